@@ -1,0 +1,267 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X SageAttention quantized path (one JSON line on stdout).
+
+Workload (BASELINE.json metric): ``sageattn`` at B=1, H=32, S=16384, D=128,
+bf16, HND, causal, smooth_k=False.  A step is one full ``sageattn`` call (V
+layout + INT8 quant of Q/K + fused INT8-QK^T/fp16-PV attention) on inputs
+already resident in HBM; ``value`` is effective TOPS of the whole step:
+4*B*H*D*S(S+1)/2 / step time.
+
+``roofline`` is the fused attention kernel alone, timed with HIP events on the
+stream it is launched on (torch's current stream): achieved = the same ops /
+average launch time, against the published dense INT8 MFMA peak of MI355X
+(5.0 POP/s).  ``cpu_baseline`` is the CPU oracle (numpy, all host cores its
+BLAS uses) on one head of the same workload, scaled to effective TOPS.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NS|C2|C3|C4|C5]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "sageattention-rdna3_amd"))
+
+METRIC = "effective attn TOPS + % gfx950 MFMA peak, D=128 S=16k causal bf16"
+PEAK_INT8_TOPS = 5000.0  # MI355X dense INT8 MFMA (published)
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (B, Hq, Hkv, S, D, dtype, layout, causal, smooth_k)
+    "NS": (1, 32, 32, 16384, 128, "bf16", "HND", True, False),
+    "C2": (1, 10, 10, 4096, 64, "fp16", "HND", False, False),
+    "C3": (2, 32, 32, 8192, 128, "bf16", "HND", True, True),
+    "C4": (1, 32, 8, 16384, 128, "fp16", "NHD", True, False),
+    "C5": (1, 40, 40, 32891, 128, "bf16", "HND", False, True),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def attn_ops(B, H, Sq, Sk, D, causal):
+    if causal:
+        n = min(Sq, Sk)
+        pairs = n * (n + 1) // 2 + max(0, Sq - Sk) * Sk
+    else:
+        pairs = Sq * Sk
+    return 4 * B * H * D * pairs
+
+
+def make_inputs(cfg, device):
+    import torch
+
+    B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
+    dtype = torch.bfloat16 if dt == "bf16" else torch.float16
+    g = torch.Generator(device=device).manual_seed(0)
+
+    def shp(h):
+        return (B, h, S, D) if layout == "HND" else (B, S, h, D)
+
+    q = torch.randn(shp(Hq), generator=g, device=device, dtype=torch.float32).to(dtype)
+    k = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32).to(dtype)
+    v = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32).to(dtype)
+    return q, k, v
+
+
+def cpu_baseline(cfg, budget_s):
+    """Time the CPU oracle on one (b, h) head of the workload: quant + V layout +
+    attention of that head; returns the cpu_baseline object."""
+    import numpy as np
+
+    sys.path.insert(0, REPO)
+    from oracle import sage_oracle as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = len(os.sched_getaffinity(0))
+    B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
+    rng = np.random.default_rng(0)
+    shp = (1, 1, S, D)
+    q, k, v = (orc.from_f32(rng.standard_normal(shp).astype(np.float32), dt) for _ in range(3))
+    t0 = time.perf_counter()
+    mean = orc.k_mean(k, dt, "HND") if smooth else None
+    q8, qs, k8, ks = orc.quant_qk_int8(q, k, dt, "HND", D ** -0.5, k_mean=mean)
+    vt = orc.v_layout(v, dt, "HND")
+    t_pro = time.perf_counter() - t0
+    # attention rows in 512-row blocks, from the last (heaviest for causal) down,
+    # until the whole head is done or the time budget is used
+    done_pairs, rows_done, t_attn = 0, 0, 0.0
+    for r1 in range(S, 0, -512):
+        rows = np.arange(max(0, r1 - 512), r1)
+        t1 = time.perf_counter()
+        orc.attn_i8_rows(q8, k8, vt, qs, ks, 0, 0, rows, causal)
+        t_attn += time.perf_counter() - t1
+        done_pairs += orc.pairs_for_rows(rows, S, causal)
+        rows_done += rows.size
+        if t_attn + t_pro > budget_s:
+            break
+    ops = 4 * D * done_pairs
+    # scale the prologue time to the rows done (it is computed for the whole head)
+    t_total = t_attn + t_pro * rows_done / S
+    return {
+        "value": ops / t_total / 1e12,
+        "unit": "TOPS",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"CPU oracle (numpy) on head 0 of 1x{Hq} heads: quant+V layout of the head "
+                   f"(pro-rated) + attention of {rows_done}/{S} query rows "
+                   f"({'causal ' if causal else ''}{done_pairs} key pairs), {t_total:.1f} s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="NS", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards by (batch, head) "
+              "with no communication, so N GPUs run N independent copies of this single-GPU line.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from sageattention import ops, sageattn
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = CONFIGS[args.config]
+    B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
+    props = torch.cuda.get_device_properties(dev)
+    log(f"[bench] device {props.name} CUs={props.multi_processor_count} config={args.config} {cfg}")
+
+    q, k, v = make_inputs(cfg, dev)
+    torch.cuda.synchronize()
+
+    def step():
+        return sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth)
+
+    for i in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done")
+
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    ops_step = attn_ops(B, Hq, S, S, D, causal)
+    value = ops_step / (ms_step * 1e-3) / 1e12
+    log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS")
+
+    # ---- per-kernel timing with HIP events on the launch stream
+    lay = ops.HND if layout == "HND" else ops.NHD
+    stream = torch.cuda.current_stream(dev)
+    mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=dev, dtype=q.dtype)
+    q8, qs, k8, ks = ops.quant_qk_int8(q, k, mean, lay, D ** -0.5)
+    vt = torch.empty(B, Hkv, D, (S + 63) // 64 * 64, device=dev, dtype=torch.float16)
+    ops.v_transpose(v, vt, lay)
+    o = torch.empty_like(q)
+
+    def timed(fn, n):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        for _ in range(3):
+            fn()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    n_k = max(args.steps, 10)
+    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5), n_k)
+    ms_quant = timed(lambda: ops.quant_qk_int8(q, k, mean, lay, D ** -0.5), n_k)
+    ms_vl = timed(lambda: ops.v_transpose(v, vt, lay), n_k)
+    ms_mean = timed(lambda: ops.mean_seq(k, lay), n_k) if smooth else 0.0
+    torch.cuda.synchronize()
+    achieved = ops_step / (ms_attn * 1e-3) / 1e12
+    nq, nk = B * Hq * S * D, B * Hkv * S * D
+    quant_bytes = 2 * (nq + nk) + (nq + nk) + 4 * (B * Hq * ((S + 31) // 32) + B * Hkv * ((S + 15) // 16))
+    vl_bytes = 2 * nk + 2 * B * Hkv * D * ((S + 63) // 64 * 64)
+    mean_bytes = 2 * nk + 2 * B * Hkv * D
+    mixed = 2.0 / (1.0 / PEAK_INT8_TOPS + 1.0 / PEAK_F16_TFLOPS)
+    log(f"[bench] attn kernel {ms_attn:.4f} ms = {achieved:.1f} TOPS ({100 * achieved / PEAK_INT8_TOPS:.1f}% INT8 peak); "
+        f"quant {ms_quant * 1e3:.1f} us = {quant_bytes / ms_quant / 1e6:.0f} GB/s; "
+        f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s")
+
+    traffic = None
+    tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("attn_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] CPU oracle baseline ...")
+        cpu = cpu_baseline(cfg, args.cpu_budget)
+        log(f"[bench] cpu {cpu['value']:.4g} TOPS on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic N(0,1) inputs generated on the GPU from seed 0",
+        "config": {
+            "workload": f"{args.config}: sageattn B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} {dt} {layout} "
+                        f"{'causal' if causal else 'non-causal'} smooth_k={smooth}",
+            "B": B, "Hq": Hq, "Hkv": Hkv, "S": S, "D": D, "io_dtype": dt, "layout": layout,
+            "causal": causal, "smooth_k": smooth, "qk": "int8 MFMA", "pv": "fp16 MFMA",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_INT8_TOPS, 4),
+            "traffic": traffic,
+            "kernel": "attn_i8_fwd_kernel",
+            "kernel_ms": round(ms_attn, 5),
+            "frac_of_mixed_int8_fp16_ceiling": round(achieved / mixed, 4),
+        },
+        "prologue": {
+            "quant_us": round(ms_quant * 1e3, 2),
+            "quant_GBps": round(quant_bytes / ms_quant / 1e6, 1),
+            "quant_frac_hbm": round(quant_bytes / ms_quant / 1e6 / PEAK_HBM_GBS, 4),
+            "v_layout_us": round(ms_vl * 1e3, 2),
+            "v_layout_GBps": round(vl_bytes / ms_vl / 1e6, 1),
+            "k_mean_us": round(ms_mean * 1e3, 2) if smooth else None,
+            "k_mean_GBps": round(mean_bytes / ms_mean / 1e6, 1) if smooth else None,
+        },
+        "device": {"name": props.name, "cus": props.multi_processor_count},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,124 @@
+/*
+ * sageattn_mi355x.h -- C ABI of the MI355X (gfx950) SageAttention quantized path.
+ *
+ * Every entry point is asynchronous on the given HIP stream (a hipStream_t
+ * passed as void*; NULL = the legacy default stream), never synchronises the
+ * host, and allocates nothing: the caller owns every buffer (inputs, outputs,
+ * workspaces).  Entry points validate their arguments before touching the GPU
+ * and return SAGE_OK (0) or a negative status; the message of the last failure
+ * on the calling thread is returned by sage_last_error().
+ *
+ * Strides are in ELEMENTS.  Tensor "layout" (HND [B,H,N,D] or NHD [B,N,H,D])
+ * is expressed only through (stride_b, stride_h, stride_n); the head_dim axis
+ * must be contiguous.  16-byte vector accesses require base pointers aligned
+ * to 16 bytes and batch/head/token strides that are multiples of 8 elements.
+ *
+ * Reference interfaces replaced (LuXuxue/sageattention-rdna3):
+ *   torch.ops.sageattention.{mean_seq, quant_qk_int8, v_transpose,
+ *   qk_int8_sv_bf16_attn_t}, declared at csrc/pybind_gfx11.cpp:18-38 and
+ *   csrc/attn_gfx11.h:10-51, implemented at csrc/attn_gfx11.cu:1889-2273.
+ */
+#ifndef SAGEATTN_MI355X_H
+#define SAGEATTN_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAGE_ABI_VERSION 1
+
+/* element types of the fp inputs / outputs */
+#define SAGE_DTYPE_F16 0
+#define SAGE_DTYPE_BF16 1
+
+/* status codes */
+#define SAGE_OK 0
+#define SAGE_ERR_INVALID_ARG (-1) /* null pointer, negative size, bad dtype, Hq % Hkv != 0 */
+#define SAGE_ERR_UNSUPPORTED (-2) /* head_dim not in {64, 128}, size beyond 32-bit grid limits */
+#define SAGE_ERR_ALIGNMENT (-3)   /* pointer or stride breaks the 16-byte access contract */
+#define SAGE_ERR_HIP (-4)         /* the HIP runtime rejected a launch */
+
+/* Quantisation granularity (tokens per fp32 scale), csrc/attn_gfx11.cu:46-47. */
+#define SAGE_Q_GROUP 32
+#define SAGE_K_GROUP 16
+/* V_T token padding, sageattention/core.py:174. */
+#define SAGE_VT_ALIGN 64
+
+/* ABI version of the loaded library (== SAGE_ABI_VERSION it was built with).
+ * No reference counterpart (the reference binds through the torch dispatcher). */
+int sage_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none).
+ * No reference counterpart (reference: Python asserts, sageattention/core.py:50-63,91-95). */
+const char* sage_last_error(void);
+
+/* Bytes of fp32 workspace sage_k_mean needs for this shape. */
+int64_t sage_k_mean_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim);
+
+/*
+ * K mean over the sequence for smooth_k: mean_out[b,h,d] = dtype(sum_s fp32(key[b,s,h,d]) / S).
+ * mean_out is contiguous [B,H,D] of `dtype`; workspace holds
+ * sage_k_mean_workspace_bytes() bytes (no initialisation needed).
+ * Replaces mean_seq (csrc/pybind_gfx11.cpp:36, csrc/attn_gfx11.h:48,
+ * csrc/attn_gfx11.cu:1937-1972; kernel :94-145).
+ */
+int sage_k_mean(const void* key, void* mean_out, void* workspace, int dtype,
+                int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                int64_t stride_b, int64_t stride_h, int64_t stride_n, void* stream);
+
+/*
+ * Per-block INT8 quantisation of Q (pre-scaled by fp32(sm_scale)*log2(e),
+ * groups of SAGE_Q_GROUP tokens) and K (minus key_mean when non-NULL, groups
+ * of SAGE_K_GROUP tokens), in one launch.
+ * Outputs (contiguous): q_i8 [B,Hq,Sq,D] int8, q_scale [B,Hq,ceil(Sq/32)] fp32,
+ * k_i8 [B,Hkv,Sk,D] int8, k_scale [B,Hkv,ceil(Sk/16)] fp32.  key_mean is
+ * contiguous [B,Hkv,D] of `dtype`.
+ * Replaces quant_qk_int8 (csrc/pybind_gfx11.cpp:32-35, csrc/attn_gfx11.h:41-46,
+ * csrc/attn_gfx11.cu:1974-2067; kernel :147-321), except that the caller
+ * allocates the four outputs.
+ */
+int sage_quant_qk_i8(const void* query, const void* key, const void* key_mean,
+                     int8_t* q_i8, float* q_scale, int8_t* k_i8, float* k_scale, int dtype,
+                     int64_t batch, int64_t q_heads, int64_t kv_heads,
+                     int64_t q_len, int64_t kv_len, int64_t head_dim,
+                     int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                     int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                     double sm_scale, void* stream);
+
+/* Token length of V_T rows: ceil(seq_len / SAGE_VT_ALIGN) * SAGE_VT_ALIGN. */
+int64_t sage_v_layout_padded_len(int64_t seq_len);
+
+/*
+ * V -> V_T fp16 [B,H,D,padded_len] contiguous, tokens contiguous, zero padded
+ * past seq_len, bf16 converted to fp16 with round-to-nearest-even.
+ * Replaces v_transpose (csrc/pybind_gfx11.cpp:37, csrc/attn_gfx11.h:51,
+ * csrc/attn_gfx11.cu:1889-1935; kernel :323-407).
+ */
+int sage_v_layout(const void* value, void* value_t, int dtype,
+                  int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                  int64_t stride_b, int64_t stride_h, int64_t stride_n, void* stream);
+
+/*
+ * Fused attention: S = (q_i8 . k_i8) * q_scale * k_scale (log2 domain), causal
+ * mask top-left (key j > query i masked), online softmax with exp2, P rounded
+ * to fp16, O = P . V_T (fp32 accumulation), out = O / rowsum cast to out_dtype.
+ * Inputs are the outputs of sage_quant_qk_i8 and sage_v_layout; GQA maps query
+ * head hq to kv head hq / (q_heads / kv_heads).  `out` is [B,Sq,Hq,D] or
+ * [B,Hq,Sq,D] by its strides (multiples of 4 elements, 8-byte aligned base).
+ * Replaces qk_int8_sv_bf16_attn_t (csrc/pybind_gfx11.cpp:19-23,
+ * csrc/attn_gfx11.h:10-19, csrc/attn_gfx11.cu:2069-2273; kernel :409-1243).
+ */
+int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
+                     const float* q_scale, const float* k_scale, int out_dtype,
+                     int64_t batch, int64_t q_heads, int64_t kv_heads,
+                     int64_t q_len, int64_t kv_len, int64_t head_dim,
+                     int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                     int is_causal, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAGEATTN_MI355X_H */

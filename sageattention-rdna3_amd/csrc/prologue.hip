@@ -1,0 +1,533 @@
+// Prologue kernels of the quantized attention path on gfx950:
+//   * per-block INT8 quantisation of Q and K (one launch for both),
+//   * the K mean for smooth_k (two small launches, deterministic order),
+//   * the V -> fp16 V_T layout transform.
+// All three are HBM-bound byte shuffles: one 16-byte load per lane per row
+// piece, wave64 reductions, 8/16-byte coalesced stores, no MFMA.
+//
+// Bit-exactness: the quantiser's arithmetic follows the reference order
+// (csrc/attn_gfx11.cu:179-321) in IEEE fp32 with contraction disabled in this
+// file (the build also passes -ffp-contract=off), true division for
+// amax/127 and 127/amax, and the reference rounding rule (:85-92).
+#pragma clang fp contract(off)
+
+#include "sage_common.h"
+
+namespace sage {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kQGroup = SAGE_Q_GROUP;  // tokens per Q scale
+constexpr int kKGroup = SAGE_K_GROUP;  // tokens per K scale
+constexpr float kAmaxFloor = 1e-7f;    // csrc/attn_gfx11.cu:192
+constexpr float kLog2e = 1.4426950408889634f;
+
+// float_to_int8 of csrc/attn_gfx11.cu:85-92: fp32 add of +-0.5, truncation
+// toward zero (v_cvt_i32_f32 semantics, NaN -> 0), clamp to [-128, 127].
+__device__ __forceinline__ int round_half_away_i8(float t) {
+  const float u = t + ((t >= 0.0f) ? 0.5f : -0.5f);
+  const float c = __builtin_fminf(__builtin_fmaxf(u, -128.0f), 127.0f);
+  const int r = static_cast<int>(c);
+  return (u == u) ? r : 0;
+}
+
+__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
+  return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+         ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int width_log2) {
+  // butterfly over lanes xor 1..2^(width_log2-1); max is order independent
+  for (int m = 1; m < (1 << width_log2); m <<= 1) v = __builtin_fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// ------------------------------------------------------------------ quant
+struct QuantParams {
+  const void* q;
+  const void* k;
+  const void* k_mean;  // [B,Hkv,D] or null
+  int8_t* q8;
+  float* q_scale;
+  int8_t* k8;
+  float* k_scale;
+  int64_t q_sb, q_sh, q_sn;
+  int64_t k_sb, k_sh, k_sn;
+  int64_t n_q_units;      // B*Hq*ceil(Sq/32)
+  int64_t n_units;        // n_q_units + B*Hkv*ceil(Sk/32)
+  int32_t hq, hkv, sq, sk;
+  int32_t q_units, k_units;  // 32-token units per head
+  int32_t q_groups, k_groups;
+  float s;  // fp32(sm_scale) * fp32(log2 e)
+};
+
+// One wave64 per 32-token unit.  Q unit = one 32-token scale group over all 64
+// lanes; K unit = two 16-token groups, one per half wave.  Lane l of half h
+// owns 16-byte column chunk `cc` of rows h*16 + rsub + i*RPI (i < ITER), so
+// every load instruction covers whole rows and every store is coalesced.
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void quant_qk_i8_kernel(QuantParams p) {
+  constexpr int CPR = D / 8;       // 16-byte chunks per row
+  constexpr int RPI = 32 / CPR;    // rows per iteration per half wave
+  constexpr int ITER = 16 / RPI;   // iterations per lane
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (unit >= p.n_units) return;
+  const bool is_q = unit < p.n_q_units;
+  const int64_t u = is_q ? unit : unit - p.n_q_units;
+  const int upb = is_q ? p.q_units : p.k_units;
+  const int H = is_q ? p.hq : p.hkv;
+  const int S = is_q ? p.sq : p.sk;
+  const int64_t bh = u / upb;
+  const int ub = static_cast<int>(u - bh * upb);
+  const int64_t b = bh / H;
+  const int64_t h = bh - b * H;
+  const int half = lane >> 5;
+  const int li = lane & 31;
+  const int cc = li % CPR;
+  const int rsub = li / CPR;
+  const int row0 = ub * 32 + half * 16 + rsub;
+
+  const uint16_t* src = static_cast<const uint16_t*>(is_q ? p.q : p.k);
+  const int64_t sb = is_q ? p.q_sb : p.k_sb;
+  const int64_t sh = is_q ? p.q_sh : p.k_sh;
+  const int64_t sn = is_q ? p.q_sn : p.k_sn;
+  const uint16_t* base = src + b * sb + h * sh + cc * 8;
+
+  uint4 raw[ITER];
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    const int row = row0 + i * RPI;
+    if (row < S) {
+      raw[i] = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(row) * sn);
+    } else {
+      raw[i] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  float mean[8];
+  const bool has_mean = (!is_q) && (p.k_mean != nullptr);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) mean[j] = 0.0f;
+  if (has_mean) {
+    const uint4 mr = *reinterpret_cast<const uint4*>(
+        static_cast<const uint16_t*>(p.k_mean) + bh * D + cc * 8);
+    const uint32_t mw[4] = {mr.x, mr.y, mr.z, mr.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float2_t f = unpack2<BF16>(mw[j]);
+      mean[2 * j] = f.x;
+      mean[2 * j + 1] = f.y;
+    }
+  }
+  const float pre = is_q ? p.s : 1.0f;
+
+  // pass 1: absmax of fl(x*s) (Q) or |fl(x - mean)| (K), floor 1e-7
+  float amax = kAmaxFloor;
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    if (row0 + i * RPI < S) {
+      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float2_t f = unpack2<BF16>(w[j]);
+        float v0 = f.x, v1 = f.y;
+        if (has_mean) {
+          v0 = v0 - mean[2 * j];
+          v1 = v1 - mean[2 * j + 1];
+        }
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(v0 * pre));
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(v1 * pre));
+      }
+    }
+  }
+  amax = wave_max_xor(amax, 5);  // within the half wave (one K group)
+  if (is_q) amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, kWave));  // whole wave (Q group)
+
+  const float scale = amax / 127.0f;
+  const float inv = 127.0f / amax;
+  const float iscale = inv * pre;
+  if (is_q) {
+    if (lane == 0) p.q_scale[bh * p.q_groups + ub] = scale;
+  } else if (li == 0) {
+    const int g = ub * 2 + half;
+    if (g * kKGroup < S) p.k_scale[bh * p.k_groups + g] = scale;
+  }
+
+  // pass 2: quantise and store 8 bytes per chunk
+  int8_t* dst = (is_q ? p.q8 : p.k8) + bh * static_cast<int64_t>(S) * D + cc * 8;
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    const int row = row0 + i * RPI;
+    if (row < S) {
+      const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+      int r8[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float2_t f = unpack2<BF16>(w[j]);
+        float v0 = f.x, v1 = f.y;
+        if (has_mean) {
+          v0 = v0 - mean[2 * j];
+          v1 = v1 - mean[2 * j + 1];
+        }
+        r8[2 * j] = round_half_away_i8(v0 * iscale);
+        r8[2 * j + 1] = round_half_away_i8(v1 * iscale);
+      }
+      uint2 o;
+      o.x = pack_i8x4(r8[0], r8[1], r8[2], r8[3]);
+      o.y = pack_i8x4(r8[4], r8[5], r8[6], r8[7]);
+      *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(row) * D) = o;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ K mean
+constexpr int kMeanChunk = 256;  // rows per stage-1 block
+
+struct MeanParams {
+  const void* k;
+  void* mean;
+  float* ws;  // [B*H, nchunks, D]
+  int64_t sb, sh, sn;
+  int32_t h, s, nchunks;
+};
+
+// Stage 1: block (chunk, h, b) sums its 256 rows per column.  Thread t owns
+// column chunk t % CPR and row slot t / CPR; slot sums are combined in slot
+// order through LDS.  The order is fixed so the result is reproducible.
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void k_mean_partial_kernel(MeanParams p) {
+  constexpr int CPR = D / 8;
+  constexpr int SLOTS = 256 / CPR;
+  constexpr int PASSES = kMeanChunk / SLOTS;
+  __shared__ float red[SLOTS][D];
+  const int t = threadIdx.x;
+  const int cc = t % CPR;
+  const int slot = t / CPR;
+  const int64_t bh = blockIdx.x / p.nchunks;
+  const int64_t chunk = blockIdx.x - bh * p.nchunks;
+  const int64_t b = bh / p.h;
+  const int64_t h = bh - b * p.h;
+  const uint16_t* base = static_cast<const uint16_t*>(p.k) + b * p.sb + h * p.sh + cc * 8;
+  const int row0 = static_cast<int>(chunk) * kMeanChunk + slot;
+
+  uint4 raw[PASSES];
+#pragma unroll
+  for (int j = 0; j < PASSES; ++j) {
+    const int row = row0 + j * SLOTS;
+    raw[j] = (row < p.s) ? *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(row) * p.sn)
+                         : make_uint4(0, 0, 0, 0);
+  }
+  float acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc[c] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PASSES; ++j) {
+    const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float2_t f = unpack2<BF16>(w[q]);
+      acc[2 * q] = acc[2 * q] + f.x;
+      acc[2 * q + 1] = acc[2 * q + 1] + f.y;
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) red[slot][cc * 8 + c] = acc[c];
+  __syncthreads();
+  if (t < D) {
+    float sum = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < SLOTS; ++r) sum = sum + red[r][t];
+    p.ws[(bh * p.nchunks + chunk) * D + t] = sum;
+  }
+}
+
+// Stage 2: one thread per (b, h, d) adds the chunk sums in chunk order.
+template <bool BF16, int D>
+__global__ __launch_bounds__(D) void k_mean_final_kernel(MeanParams p) {
+  const int t = threadIdx.x;
+  const int64_t bh = blockIdx.x;
+  const float* w = p.ws + bh * p.nchunks * D + t;
+  float sum = 0.0f;
+  for (int c = 0; c < p.nchunks; ++c) sum = sum + w[static_cast<int64_t>(c) * D];
+  const float m = sum / static_cast<float>(p.s);
+  uint16_t out;
+  if constexpr (BF16) {
+    out = static_cast<uint16_t>(pack_bf16x2(m, 0.0f) & 0xffffu);
+  } else {
+    out = static_cast<uint16_t>(pack_f16x2(m, 0.0f) & 0xffffu);
+  }
+  static_cast<uint16_t*>(p.mean)[bh * D + t] = out;
+}
+
+// ------------------------------------------------------------------ V layout
+constexpr int kVTile = 64;  // tokens per block (== SAGE_VT_ALIGN)
+
+struct VLayoutParams {
+  const void* v;
+  uint16_t* vt;  // fp16 [B,H,D,NP]
+  int64_t sb, sh, sn;
+  int64_t np;
+  int32_t h, s, ntiles;
+};
+
+// Block = (64-token tile, b*h).  Thread loads two consecutive tokens x 8
+// channels (two 16-byte loads, whole rows per wave), interleaves them into
+// token-pair dwords in LDS [D][32 pairs], then stores 8 consecutive tokens
+// (16 bytes) per channel row of V_T.  bf16 -> fp16 conversion is fused.
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void v_layout_kernel(VLayoutParams p) {
+  constexpr int CPR = D / 8;                        // chunks per token row
+  constexpr int PAIRS = kVTile / 2;                 // token pairs per tile
+  constexpr int LOAD_TASKS = PAIRS * CPR;           // (pair, chunk) tasks
+  constexpr int LOADS = LOAD_TASKS / 256;
+  constexpr int STORE_TASKS = D * (kVTile / 8);     // (channel, 8-token) tasks
+  constexpr int STORES = STORE_TASKS / 256;
+  constexpr int LSTRIDE = PAIRS + 4;                // dwords per channel row (pad)
+  __shared__ __align__(16) uint32_t tile[D * LSTRIDE];
+
+  const int t = threadIdx.x;
+  const int64_t bh = blockIdx.x / p.ntiles;
+  const int tile_n = static_cast<int>(blockIdx.x - bh * p.ntiles);
+  const int64_t b = bh / p.h;
+  const int64_t h = bh - b * p.h;
+  const int n0 = tile_n * kVTile;
+  const uint16_t* base = static_cast<const uint16_t*>(p.v) + b * p.sb + h * p.sh;
+
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int task = t + i * 256;
+    const int cc = task % CPR;
+    const int pr = task / CPR;
+    const int n = n0 + 2 * pr;
+    uint4 a = make_uint4(0, 0, 0, 0), c = make_uint4(0, 0, 0, 0);
+    if (n < p.s) a = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(n) * p.sn + cc * 8);
+    if (n + 1 < p.s) c = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(n + 1) * p.sn + cc * 8);
+    const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
+    const uint32_t wc[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t lo, hi;  // lo: channels 2q of tokens (n, n+1); hi: channel 2q+1
+      if constexpr (BF16) {
+        const float2_t fa = unpack2<true>(wa[q]);
+        const float2_t fc = unpack2<true>(wc[q]);
+        lo = pack_f16x2(fa.x, fc.x);
+        hi = pack_f16x2(fa.y, fc.y);
+      } else {
+        lo = (wa[q] & 0xffffu) | (wc[q] << 16);
+        hi = (wa[q] >> 16) | (wc[q] & 0xffff0000u);
+      }
+      tile[(cc * 8 + 2 * q) * LSTRIDE + pr] = lo;
+      tile[(cc * 8 + 2 * q + 1) * LSTRIDE + pr] = hi;
+    }
+  }
+  __syncthreads();
+  uint16_t* out = p.vt + bh * D * p.np + n0;
+#pragma unroll
+  for (int i = 0; i < STORES; ++i) {
+    const int task = t + i * 256;
+    const int n8 = task % (kVTile / 8);
+    const int d = task / (kVTile / 8);
+    const uint32_t* s = &tile[d * LSTRIDE + n8 * 4];
+    uint4 w;
+    w.x = s[0];
+    w.y = s[1];
+    w.z = s[2];
+    w.w = s[3];
+    *reinterpret_cast<uint4*>(out + static_cast<int64_t>(d) * p.np + n8 * 8) = w;
+  }
+}
+
+// ------------------------------------------------------------------ checks
+int check_dtype(int dtype) {
+  if (dtype != SAGE_DTYPE_F16 && dtype != SAGE_DTYPE_BF16)
+    return set_error(SAGE_ERR_INVALID_ARG, "dtype must be SAGE_DTYPE_F16 or SAGE_DTYPE_BF16, got %d", dtype);
+  return SAGE_OK;
+}
+
+int check_head_dim(int64_t d) {
+  if (d != 64 && d != 128)
+    return set_error(SAGE_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld", static_cast<long long>(d));
+  return SAGE_OK;
+}
+
+int check_strides(const char* name, const void* ptr, int64_t sb, int64_t sh, int64_t sn) {
+  if (!aligned(ptr, 16))
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: base pointer must be 16-byte aligned", name);
+  if ((sb % 8) || (sh % 8) || (sn % 8))
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: strides (b=%lld, h=%lld, n=%lld) must be multiples of 8 elements",
+                     name, static_cast<long long>(sb), static_cast<long long>(sh), static_cast<long long>(sn));
+  return SAGE_OK;
+}
+
+}  // namespace
+}  // namespace sage
+
+using namespace sage;
+
+extern "C" int sage_quant_qk_i8(const void* query, const void* key, const void* key_mean,
+                                int8_t* q_i8, float* q_scale, int8_t* k_i8, float* k_scale, int dtype,
+                                int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                                double sm_scale, void* stream) {
+  clear_error();
+  int rc;
+  if ((rc = check_dtype(dtype)) || (rc = check_head_dim(head_dim))) return rc;
+  if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || q_len < 0 || kv_len < 0)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_quant_qk_i8: negative or zero size");
+  if (q_len > INT32_MAX || kv_len > INT32_MAX || q_heads > INT32_MAX || kv_heads > INT32_MAX)
+    return set_error(SAGE_ERR_UNSUPPORTED, "sage_quant_qk_i8: sizes beyond 32-bit limits");
+  const bool do_q = batch > 0 && q_len > 0;
+  const bool do_k = batch > 0 && kv_len > 0;
+  if (do_q && (!query || !q_i8 || !q_scale))
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_quant_qk_i8: null query/q_i8/q_scale");
+  if (do_k && (!key || !k_i8 || !k_scale))
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_quant_qk_i8: null key/k_i8/k_scale");
+  if (do_q && ((rc = check_strides("query", query, q_stride_b, q_stride_h, q_stride_n)))) return rc;
+  if (do_k && ((rc = check_strides("key", key, k_stride_b, k_stride_h, k_stride_n)))) return rc;
+  if (do_k && key_mean && !aligned(key_mean, 16))
+    return set_error(SAGE_ERR_ALIGNMENT, "key_mean: base pointer must be 16-byte aligned");
+  if ((do_q && !aligned(q_i8, 8)) || (do_k && !aligned(k_i8, 8)) || (do_q && !aligned(q_scale, 4)) ||
+      (do_k && !aligned(k_scale, 4)))
+    return set_error(SAGE_ERR_ALIGNMENT, "sage_quant_qk_i8: int8 outputs need 8-byte, scales 4-byte alignment");
+
+  QuantParams p;
+  p.q = query;
+  p.k = key;
+  p.k_mean = key_mean;
+  p.q8 = q_i8;
+  p.q_scale = q_scale;
+  p.k8 = k_i8;
+  p.k_scale = k_scale;
+  p.q_sb = q_stride_b;
+  p.q_sh = q_stride_h;
+  p.q_sn = q_stride_n;
+  p.k_sb = k_stride_b;
+  p.k_sh = k_stride_h;
+  p.k_sn = k_stride_n;
+  p.hq = static_cast<int32_t>(q_heads);
+  p.hkv = static_cast<int32_t>(kv_heads);
+  p.sq = static_cast<int32_t>(q_len);
+  p.sk = static_cast<int32_t>(kv_len);
+  p.q_units = static_cast<int32_t>(cdiv(q_len, 32));
+  p.k_units = static_cast<int32_t>(cdiv(kv_len, 32));
+  p.q_groups = static_cast<int32_t>(cdiv(q_len, kQGroup));
+  p.k_groups = static_cast<int32_t>(cdiv(kv_len, kKGroup));
+  p.n_q_units = do_q ? batch * q_heads * p.q_units : 0;
+  p.n_units = p.n_q_units + (do_k ? batch * kv_heads * p.k_units : 0);
+  p.s = static_cast<float>(sm_scale) * kLog2e;
+  if (p.n_units == 0) return SAGE_OK;
+  const int64_t blocks = cdiv(p.n_units, 4);
+  if (blocks > INT32_MAX) return set_error(SAGE_ERR_UNSUPPORTED, "sage_quant_qk_i8: grid too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  if (dtype == SAGE_DTYPE_BF16) {
+    if (head_dim == 128) quant_qk_i8_kernel<true, 128><<<grid, block, 0, st>>>(p);
+    else quant_qk_i8_kernel<true, 64><<<grid, block, 0, st>>>(p);
+  } else {
+    if (head_dim == 128) quant_qk_i8_kernel<false, 128><<<grid, block, 0, st>>>(p);
+    else quant_qk_i8_kernel<false, 64><<<grid, block, 0, st>>>(p);
+  }
+  return check_launch("sage_quant_qk_i8");
+}
+
+extern "C" int64_t sage_k_mean_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim) {
+  if (batch <= 0 || heads <= 0 || seq_len <= 0 || head_dim <= 0) return 0;
+  return batch * heads * cdiv(seq_len, kMeanChunk) * head_dim * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int sage_k_mean(const void* key, void* mean_out, void* workspace, int dtype,
+                           int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                           int64_t stride_b, int64_t stride_h, int64_t stride_n, void* stream) {
+  clear_error();
+  int rc;
+  if ((rc = check_dtype(dtype)) || (rc = check_head_dim(head_dim))) return rc;
+  if (batch < 0 || heads <= 0 || seq_len < 0)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_k_mean: negative or zero size");
+  if (batch == 0) return SAGE_OK;
+  if (seq_len == 0)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_k_mean: mean over an empty sequence");
+  if (seq_len > INT32_MAX || heads > INT32_MAX ||
+      batch * heads * cdiv(seq_len, kMeanChunk) > INT32_MAX)
+    return set_error(SAGE_ERR_UNSUPPORTED, "sage_k_mean: sizes beyond grid limits");
+  if (!key || !mean_out || !workspace)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_k_mean: null key/mean_out/workspace");
+  if ((rc = check_strides("key", key, stride_b, stride_h, stride_n))) return rc;
+  if (!aligned(workspace, 4) || !aligned(mean_out, 2))
+    return set_error(SAGE_ERR_ALIGNMENT, "sage_k_mean: misaligned workspace or output");
+  MeanParams p;
+  p.k = key;
+  p.mean = mean_out;
+  p.ws = static_cast<float*>(workspace);
+  p.sb = stride_b;
+  p.sh = stride_h;
+  p.sn = stride_n;
+  p.h = static_cast<int32_t>(heads);
+  p.s = static_cast<int32_t>(seq_len);
+  p.nchunks = static_cast<int32_t>(cdiv(seq_len, kMeanChunk));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 g1(static_cast<uint32_t>(batch * heads * p.nchunks));
+  const dim3 g2(static_cast<uint32_t>(batch * heads));
+  if (dtype == SAGE_DTYPE_BF16) {
+    if (head_dim == 128) {
+      k_mean_partial_kernel<true, 128><<<g1, 256, 0, st>>>(p);
+      k_mean_final_kernel<true, 128><<<g2, 128, 0, st>>>(p);
+    } else {
+      k_mean_partial_kernel<true, 64><<<g1, 256, 0, st>>>(p);
+      k_mean_final_kernel<true, 64><<<g2, 64, 0, st>>>(p);
+    }
+  } else {
+    if (head_dim == 128) {
+      k_mean_partial_kernel<false, 128><<<g1, 256, 0, st>>>(p);
+      k_mean_final_kernel<false, 128><<<g2, 128, 0, st>>>(p);
+    } else {
+      k_mean_partial_kernel<false, 64><<<g1, 256, 0, st>>>(p);
+      k_mean_final_kernel<false, 64><<<g2, 64, 0, st>>>(p);
+    }
+  }
+  return check_launch("sage_k_mean");
+}
+
+extern "C" int64_t sage_v_layout_padded_len(int64_t seq_len) {
+  if (seq_len <= 0) return 0;
+  return cdiv(seq_len, SAGE_VT_ALIGN) * SAGE_VT_ALIGN;
+}
+
+extern "C" int sage_v_layout(const void* value, void* value_t, int dtype,
+                             int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                             int64_t stride_b, int64_t stride_h, int64_t stride_n, void* stream) {
+  clear_error();
+  int rc;
+  if ((rc = check_dtype(dtype)) || (rc = check_head_dim(head_dim))) return rc;
+  if (batch < 0 || heads <= 0 || seq_len < 0)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_v_layout: negative or zero size");
+  if (batch == 0 || seq_len == 0) return SAGE_OK;
+  if (seq_len > INT32_MAX || heads > INT32_MAX ||
+      batch * heads * (sage_v_layout_padded_len(seq_len) / kVTile) > INT32_MAX)
+    return set_error(SAGE_ERR_UNSUPPORTED, "sage_v_layout: sizes beyond grid limits");
+  if (!value || !value_t) return set_error(SAGE_ERR_INVALID_ARG, "sage_v_layout: null value/value_t");
+  if ((rc = check_strides("value", value, stride_b, stride_h, stride_n))) return rc;
+  if (!aligned(value_t, 16)) return set_error(SAGE_ERR_ALIGNMENT, "value_t: base pointer must be 16-byte aligned");
+  VLayoutParams p;
+  p.v = value;
+  p.vt = static_cast<uint16_t*>(value_t);
+  p.sb = stride_b;
+  p.sh = stride_h;
+  p.sn = stride_n;
+  p.np = sage_v_layout_padded_len(seq_len);
+  p.h = static_cast<int32_t>(heads);
+  p.s = static_cast<int32_t>(seq_len);
+  p.ntiles = static_cast<int32_t>(p.np / kVTile);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(batch * heads * p.ntiles));
+  if (dtype == SAGE_DTYPE_BF16) {
+    if (head_dim == 128) v_layout_kernel<true, 128><<<grid, 256, 0, st>>>(p);
+    else v_layout_kernel<true, 64><<<grid, 256, 0, st>>>(p);
+  } else {
+    if (head_dim == 128) v_layout_kernel<false, 128><<<grid, 256, 0, st>>>(p);
+    else v_layout_kernel<false, 64><<<grid, 256, 0, st>>>(p);
+  }
+  return check_launch("sage_v_layout");
+}

@@ -1,0 +1,133 @@
+"""Op-level API mirroring the reference's ``torch.ops.sageattention`` ops.
+
+Same names, argument meaning and output shapes as the reference op layer
+(csrc/pybind_gfx11.cpp:18-38, csrc/attn_gfx11.h:10-51); each op runs the gfx950
+kernel behind the matching C-ABI entry point on the tensors' current HIP
+stream.  ``tensor_layout`` is the reference's integer code: 1 = HND
+([B,H,N,D]), 0 = NHD ([B,N,H,D]) (csrc/attn_gfx11.cu:32-33).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List
+
+import torch
+
+from . import _capi
+
+HND = 1
+NHD = 0
+
+_DTYPES = {torch.float16: _capi.DTYPE_F16, torch.bfloat16: _capi.DTYPE_BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"expected fp16 or bf16 tensor, got {t.dtype}") from None
+
+
+def _bhnd(t: torch.Tensor, tensor_layout: int):
+    """(B, H, N, D) sizes and (stride_b, stride_h, stride_n) of a 4-D tensor."""
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D tensor, got shape {tuple(t.shape)}")
+    if tensor_layout == HND:
+        return (t.size(0), t.size(1), t.size(2), t.size(3)), (t.stride(0), t.stride(1), t.stride(2))
+    return (t.size(0), t.size(2), t.size(1), t.size(3)), (t.stride(0), t.stride(2), t.stride(1))
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def mean_seq(input: torch.Tensor, tensor_layout: int) -> torch.Tensor:
+    """K mean over the sequence -> [B,H,D] of input's dtype (reference mean_seq,
+    csrc/attn_gfx11.cu:1937-1972)."""
+    (B, H, S, D), (sb, sh, sn) = _bhnd(input, tensor_layout)
+    out = torch.empty((B, H, D), dtype=input.dtype, device=input.device)
+    lib = _capi.load()
+    ws_bytes = lib.sage_k_mean_workspace_bytes(B, H, S, D)
+    ws = torch.empty((max(ws_bytes, 4) + 3) // 4, dtype=torch.float32, device=input.device)
+    with torch.cuda.device(input.device):
+        _capi.call("sage_k_mean", _ptr(input), _ptr(out), _ptr(ws), _dtype_code(input),
+                   B, H, S, D, sb, sh, sn, _stream(input))
+    return out
+
+
+def quant_qk_int8(query: torch.Tensor, key: torch.Tensor, key_mean: torch.Tensor,
+                  tensor_layout: int, sm_scale: float) -> List[torch.Tensor]:
+    """Per-block INT8 quantisation -> [q_int8, q_scale, k_int8, k_scale] (reference
+    quant_qk_int8, csrc/attn_gfx11.cu:1974-2067).  ``key_mean`` empty -> no
+    smoothing (csrc/attn_gfx11.cu:1996)."""
+    (B, Hq, Sq, D), (qsb, qsh, qsn) = _bhnd(query, tensor_layout)
+    (Bk, Hkv, Sk, Dk), (ksb, ksh, ksn) = _bhnd(key, tensor_layout)
+    if Bk != B or Dk != D:
+        raise ValueError(f"query {tuple(query.shape)} and key {tuple(key.shape)} disagree")
+    if query.dtype != key.dtype:
+        raise ValueError("query and key must have the same dtype")
+    dev = query.device
+    q8 = torch.empty((B, Hq, Sq, D), dtype=torch.int8, device=dev)
+    k8 = torch.empty((B, Hkv, Sk, D), dtype=torch.int8, device=dev)
+    qs = torch.empty((B, Hq, (Sq + 31) // 32), dtype=torch.float32, device=dev)
+    ks = torch.empty((B, Hkv, (Sk + 15) // 16), dtype=torch.float32, device=dev)
+    has_mean = key_mean is not None and key_mean.numel() > 0
+    if has_mean:
+        if tuple(key_mean.shape) != (B, Hkv, D) or key_mean.dtype != key.dtype:
+            raise ValueError(f"key_mean must be [{B},{Hkv},{D}] of {key.dtype}")
+        key_mean = key_mean.contiguous()
+    mean_ptr = _ptr(key_mean) if has_mean else ctypes.c_void_p(0)
+    with torch.cuda.device(dev):
+        _capi.call("sage_quant_qk_i8", _ptr(query), _ptr(key), mean_ptr,
+                   _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _dtype_code(query),
+                   B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, ksb, ksh, ksn,
+                   float(sm_scale), _stream(query))
+    return [q8, qs, k8, ks]
+
+
+def v_transpose(value: torch.Tensor, value_t: torch.Tensor, tensor_layout: int) -> torch.Tensor:
+    """V -> fp16 V_T [B,H,D,ceil64(N)] written into ``value_t`` (reference
+    v_transpose, csrc/attn_gfx11.cu:1889-1935)."""
+    (B, H, S, D), (sb, sh, sn) = _bhnd(value, tensor_layout)
+    NP = (S + 63) // 64 * 64
+    if (tuple(value_t.shape) != (B, H, D, NP) or value_t.dtype != torch.float16
+            or not value_t.is_contiguous()):
+        raise ValueError(f"value_t must be contiguous fp16 [{B},{H},{D},{NP}]")
+    with torch.cuda.device(value.device):
+        _capi.call("sage_v_layout", _ptr(value), _ptr(value_t), _dtype_code(value),
+                   B, H, S, D, sb, sh, sn, _stream(value))
+    return value_t
+
+
+def qk_int8_sv_bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                           output: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
+                           tensor_layout: int, is_causal: int, sm_scale: float) -> torch.Tensor:
+    """Fused attention over quantised Q/K and V_T into ``output`` (reference
+    qk_int8_sv_bf16_attn_t, csrc/attn_gfx11.cu:2069-2273).  ``sm_scale`` is
+    unused: it is already folded into ``q_scale`` (as in the reference)."""
+    B, Hq, Sq, D = query.shape
+    Bk, Hkv, Sk, Dk = key.shape
+    if Bk != B or Dk != D:
+        raise ValueError("query/key int8 tensors disagree")
+    for name, t in (("query", query), ("key", key)):
+        if t.dtype != torch.int8 or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous int8 [B,H,N,D]")
+    NP = (Sk + 63) // 64 * 64
+    if tuple(value.shape) != (B, Hkv, D, NP) or value.dtype != torch.float16 or not value.is_contiguous():
+        raise ValueError(f"value must be contiguous fp16 V_T [{B},{Hkv},{D},{NP}]")
+    if (tuple(q_scale.shape) != (B, Hq, (Sq + 31) // 32) or tuple(k_scale.shape) != (B, Hkv, (Sk + 15) // 16)
+            or q_scale.dtype != torch.float32 or k_scale.dtype != torch.float32
+            or not q_scale.is_contiguous() or not k_scale.is_contiguous()):
+        raise ValueError("q_scale/k_scale must be contiguous fp32 [B,H,ceil(N/32)] / [B,H,ceil(N/16)]")
+    (Bo, Ho, So, Do), (osb, osh, osn) = _bhnd(output, tensor_layout)
+    if (Bo, Ho, So, Do) != (B, Hq, Sq, D) or output.stride(-1) != 1:
+        raise ValueError("output shape does not match the query")
+    with torch.cuda.device(query.device):
+        _capi.call("sage_attn_i8_fwd", _ptr(query), _ptr(key), _ptr(value), _ptr(output),
+                   _ptr(q_scale), _ptr(k_scale), _dtype_code(output),
+                   B, Hq, Hkv, Sq, Sk, D, osb, osh, osn, int(bool(is_causal)), _stream(query))
+    return output
