@@ -6,9 +6,11 @@ INT8 inputs) within
     |gpu - oracle| <= ATOL + RTOL * |oracle|,  cos >= 0.99999
 (fp16 out: ATOL 2e-3, RTOL 4e-3; bf16 out: ATOL 4e-3, RTOL 1.6e-2 -- one to
 two output ulps plus online-softmax / hardware-exp2 rounding), and with fp32
-SDPA within cos >= 0.999 and the per-config max-abs below (C5's x20 outlier
-channels make the INT8 algorithm itself reach ~0.8 vs SDPA; the oracle shows
-the same).  Full BASELINE sizes compare every prologue element and a sample
+SDPA within cos >= 0.999 and max-abs <= 0.1, except C5: its x20 outlier
+channels put the INT8 algorithm itself (the oracle, no GPU involved) at cos
+~0.9975 and max-abs ~0.8 vs SDPA, so C5 is held to cos >= 0.995 and max-abs
+<= 1.0.  In every config the GPU must also be no further from SDPA than the
+oracle is (cos within 2e-5 of the oracle's).  Full BASELINE sizes compare every prologue element and a sample
 of attention rows (rows are independent).
 """
 import ctypes
@@ -26,6 +28,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = {"fp16": (2e-3, 4e-3), "bf16": (4e-3, 1.6e-2)}
 SDPA_MAXABS = {"C5": 1.0}
+SDPA_COS = {"C5": 0.995}
 
 
 def _say(*a):
@@ -141,17 +144,23 @@ def test_baseline_config_parity(cfg):
     rows = sample_rows(cfg.q_len, 48, rng)
     heads = sorted({0, cfg.Hq - 1, int(rng.integers(0, cfg.Hq))})
     worst = check_rows_vs_oracle(cfg, pro, o, heads, rows, cfg.dtype)
-    # vs fp32 SDPA on the same rows
+    # vs fp32 SDPA on the same rows, next to the oracle's own distance from SDPA
     qh, kh, vh = (orc.to_hnd(np_to_f32(to_np(t), cfg.dtype), cfg.layout) for t in (q, k, v))
     og = orc.to_hnd(np_to_f32(to_np(o), cfg.dtype), cfg.layout)
+    q8, qs, k8, ks, vt = (to_np(pro[n]) for n in ("q8", "q_scale", "k8", "k_scale", "v_t"))
     G = cfg.Hq // cfg.Hkv
-    cs, ma = [], 0.0
+    cs, cs_orc, ma = [], [], 0.0
     for h in heads:
         ref = sdpa_rows_fp32(qh[0, h], kh[0, h // G], vh[0, h // G], rows, cfg.causal, cfg.D ** -0.5)
+        orc_rows = orc.attn_i8_rows(q8, k8, vt, qs, ks, 0, h, rows, cfg.causal)
+        orc_rows = np_to_f32(orc.from_f32(orc_rows.astype(np.float32), cfg.dtype), cfg.dtype)
         cs.append(cos_sim(og[0, h, rows], ref))
+        cs_orc.append(cos_sim(orc_rows, ref))
         ma = max(ma, max_abs(og[0, h, rows], ref))
-    _say(f"  worst |gpu-oracle| = {worst:.3g}; vs fp32 SDPA: min cos {min(cs):.6f}, max-abs {ma:.4g}")
-    assert min(cs) >= 0.999
+    _say(f"  worst |gpu-oracle| = {worst:.3g}; vs fp32 SDPA: min cos {min(cs):.6f} "
+         f"(oracle {min(cs_orc):.6f}), max-abs {ma:.4g}")
+    assert min(cs) >= SDPA_COS.get(cfg.name, 0.999)
+    assert all(c >= co - 2e-5 for c, co in zip(cs, cs_orc))
     assert ma <= SDPA_MAXABS.get(cfg.name, 0.1)
 
 
