@@ -7,7 +7,9 @@ Flags:
   * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` on every device
     compile: no packed fp32 VALU instructions are generated;
   * ``-ffp-contract=off`` on the prologue (its quantiser is bit-exact IEEE
-    fp32 and must not fuse multiply-adds); no ``-ffast-math`` anywhere.
+    fp32 and must not fuse multiply-adds); no ``-ffast-math`` anywhere;
+  * ``-mllvm -amdgpu-mfma-vgpr-form`` on the attention kernel (MFMA
+    accumulators in arch VGPRs, no per-tile AGPR copies).
 """
 from __future__ import annotations
 
@@ -43,7 +45,9 @@ COMMON = [
 SOURCES = [
     ("capi.cpp", []),
     ("prologue.hip", ["-ffp-contract=off"]),
-    ("attn_i8.hip", []),
+    # MFMA results in arch VGPRs: the softmax reads every S element and the
+    # rare O rescale touches O; AGPR residency costs v_accvgpr copies per tile
+    ("attn_i8.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
 ]
 
 

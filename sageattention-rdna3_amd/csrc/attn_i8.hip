@@ -35,6 +35,7 @@ constexpr int kBN = 64;
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kXcds = 8;  // MI355X: workgroups are dealt round-robin to 8 XCDs
+constexpr float kRescale = 8.0f;  // lazy-rescale threshold of the running max (log2 units)
 
 struct AttnParams {
   const int8_t* q8;      // [B,Hq,Sq,D]
@@ -79,10 +80,17 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 
 template <int D>
 __device__ __forceinline__ void load_tile_regs(const AttnParams& p, const int8_t* kbase,
-                                               const uint16_t* vbase, int kt, int tid,
+                                               const uint16_t* vbase, const float* ksp, int kt, int tid,
                                                uint4 (&kr)[Cfg<D>::kKChunks],
-                                               uint4 (&vr)[Cfg<D>::kVChunks]) {
+                                               uint4 (&vr)[Cfg<D>::kVChunks], float (&ks)[4]) {
   using C = Cfg<D>;
+  // the tile's 4 key-group scales (same address in every lane: one broadcast);
+  // groups past the end repeat the last one and only meet masked keys
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int gi = kt / 16 + g;
+    ks[g] = ksp[gi < p.k_groups ? gi : p.k_groups - 1];
+  }
 #pragma unroll
   for (int i = 0; i < C::kKChunks; ++i) {
     const int c = tid + i * kThreads;
@@ -128,6 +136,112 @@ __device__ __forceinline__ void store_tile_lds(char* stage, int tid, const uint4
   }
 }
 
+// One 64-key tile of one wave: S^T = K.Q^T (int8 MFMA), dequant, optional
+// mask, online softmax, O^T += V^T.P^T (fp16 MFMA).  MASK selects the tail /
+// diagonal version; the steady-state tiles run the unmasked one.
+template <int D, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void attn_tile(const AttnParams& p, const char* stage, const int4_t (&qf)[Cfg<D>::kDS],
+                                          const float (&ks)[4], float qs, int kt, int qrow, int m, int hh,
+                                          float16_t_ (&o)[Cfg<D>::kDB], float& m_run, float& l_run) {
+  using C = Cfg<D>;
+  // ---- S^T = K . Q^T  (2 blocks of 32 keys)
+  int16_t_ acc[2];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[nb][r] = 0;
+    const char* krow = stage + (nb * 32 + m) * C::kKStride + hh * 16;
+#pragma unroll
+    for (int ds = 0; ds < C::kDS; ++ds) {
+      const int4_t a = *reinterpret_cast<const int4_t*>(krow + ds * 32);
+      acc[nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[ds], acc[nb], 0, 0, 0);
+    }
+  }
+  // ---- dequant scales of the 4 key groups: fl(q_scale * k_scale)
+  float sc[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) sc[g] = qs * ks[g];
+  // ---- mask: dead entries become INT32_MIN, which no real dot product
+  // reaches (|acc| <= 128*128*D < 2^22)
+  if constexpr (MASK) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int n = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        const bool dead = (n >= p.sk) || (CAUSAL && n > qrow);
+        acc[nb][r] = dead ? INT32_MIN : acc[nb][r];
+      }
+    }
+  }
+  // ---- row max: integer max inside each 16-key group, then one scale per
+  // group (x -> x*sc is monotonic for sc > 0, so this is max_j fl(acc*sc))
+  float mx = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    int gm = acc[g >> 1][(g & 1) * 8];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) gm = max(gm, acc[g >> 1][(g & 1) * 8 + r]);
+    float gv = static_cast<float>(gm) * sc[g];
+    if constexpr (MASK) gv = (gm == INT32_MIN) ? -INFINITY : gv;
+    mx = __builtin_fmaxf(mx, gv);
+  }
+  mx = xhalf_max(mx);
+  // ---- lazy rescale: the reference max only moves when some row's max grew
+  // by more than kRescale (log2 units), so p = exp2(s - m_run) stays below
+  // 2^kRescale (no fp16 overflow) and O is rescaled only on those tiles.
+  if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescale) != 0) {
+    // keeps the block a real branch: without it the 64 multiplies of O are
+    // speculated onto every tile (they are only 4 vector ops in the IR)
+    asm volatile("" ::: "memory");
+    float m_new = __builtin_fmaxf(m_run, mx);
+    m_new = (m_new == -INFINITY) ? 0.0f : m_new;
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int db = 0; db < C::kDB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+    }
+  }
+  // ---- p = exp2(acc*sc - m_run): dequant and max subtraction in one FMA
+  float s[2][16];
+  float lsum = 0.0f;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float e = fast_exp2(__builtin_fmaf(static_cast<float>(acc[nb][r]), sc[nb * 2 + (r >> 3)], -m_run));
+      if constexpr (MASK) e = (acc[nb][r] == INT32_MIN) ? 0.0f : e;
+      s[nb][r] = e;
+      lsum += e;
+    }
+  }
+  l_run += lsum;
+  // ---- P^T fragments (fp16 RNE) straight from the accumulators
+  half8_t pf[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float* sv = &s[t >> 1][(t & 1) * 8];
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = pack_f16x2(sv[2 * j], sv[2 * j + 1]);
+    pf[t] = __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
+  }
+  // ---- O^T += V^T . P^T
+  const uint16_t* vs = reinterpret_cast<const uint16_t*>(stage + C::kKBytes);
+#pragma unroll
+  for (int db = 0; db < C::kDB; ++db) {
+    const uint16_t* vrow = vs + (db * 32 + m) * C::kVStride + hh * 8;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const half8_t a = *reinterpret_cast<const half8_t*>(vrow + t * 16);
+      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[t], o[db], 0, 0, 0);
+    }
+  }
+}
+
 template <int D, bool CAUSAL, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   using C = Cfg<D>;
@@ -148,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   const int q0 = qb * kBM;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int m = lane & 31;
   const int hh = lane >> 5;
@@ -188,107 +302,40 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
 
   uint4 kr[C::kKChunks];
   uint4 vr[C::kVChunks];
+  float ks[4], ks_next[4];
   if (kv_end > 0) {
-    load_tile_regs<D>(p, kbase, vbase, 0, tid, kr, vr);
+    load_tile_regs<D>(p, kbase, vbase, ksp, 0, tid, kr, vr, ks);
     store_tile_lds<D>(smem, tid, kr, vr);
   }
   __syncthreads();
 
+  // tiles [0, main_end) need no mask for any wave of the block: fully inside
+  // the key range and (causal) entirely at or left of the block's first row
+  const int main_end = CAUSAL ? min(q0, p.sk / kBN * kBN) : p.sk / kBN * kBN;
   int it = 0;
-  for (int kt = 0; kt < kv_end; kt += kBN, ++it) {
+  int kt = 0;
+  for (; kt < main_end; kt += kBN, ++it) {
     const bool has_next = kt + kBN < kv_end;
-    if (has_next) load_tile_regs<D>(p, kbase, vbase, kt + kBN, tid, kr, vr);
-    const char* stage = smem + (it & 1) * C::kStage;
-    const bool wave_live = !CAUSAL || kt <= wrow0 + 31;
-    if (wave_live) {
-      // ---- S^T = K . Q^T  (2 blocks of 32 keys)
-      int16_t_ acc[2];
+    if (has_next) load_tile_regs<D>(p, kbase, vbase, ksp, kt + kBN, tid, kr, vr, ks_next);
+    attn_tile<D, CAUSAL, false>(p, smem + (it & 1) * C::kStage, qf, ks, qs, kt, qrow, m, hh, o, m_run, l_run);
+    if (has_next) {
+      store_tile_lds<D>(smem + ((it + 1) & 1) * C::kStage, tid, kr, vr);
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[nb][r] = 0;
-        const char* krow = stage + (nb * 32 + m) * C::kKStride + hh * 16;
-#pragma unroll
-        for (int ds = 0; ds < C::kDS; ++ds) {
-          const int4_t a = *reinterpret_cast<const int4_t*>(krow + ds * 32);
-          acc[nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[ds], acc[nb], 0, 0, 0);
-        }
-      }
-      // ---- dequant + mask
-      float sc[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int gi = kt / 16 + g;
-        sc[g] = qs * ksp[gi < p.k_groups ? gi : p.k_groups - 1];
-      }
-      float s[2][16];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[nb][r] = static_cast<float>(acc[nb][r]) * sc[nb * 2 + (r >> 3)];
-      }
-      const bool need_mask = (kt + kBN > p.sk) || (CAUSAL && kt + kBN - 1 > wrow0);
-      if (need_mask) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int n = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-            const bool dead = (n >= p.sk) || (CAUSAL && n > qrow);
-            if (dead) s[nb][r] = -INFINITY;
-          }
-        }
-      }
-      // ---- online softmax (exp2 domain)
-      float mx = s[0][0];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, s[nb][r]);
-      }
-      mx = xhalf_max(mx);
-      const float m_new = __builtin_fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-      float lsum = 0.0f;
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[nb][r] = fast_exp2(s[nb][r] - m_use);
-          lsum += s[nb][r];
-        }
-      }
-      l_run = l_run * alpha + lsum;
-#pragma unroll
-      for (int db = 0; db < C::kDB; ++db) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-      }
-      // ---- P^T fragments (fp16 RNE) straight from the accumulators
-      half8_t pf[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float* sv = &s[t >> 1][(t & 1) * 8];
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) w[j] = pack_f16x2(sv[2 * j], sv[2 * j + 1]);
-        pf[t] = __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
-      }
-      // ---- O^T += V^T . P^T
-      const uint16_t* vs = reinterpret_cast<const uint16_t*>(stage + C::kKBytes);
-#pragma unroll
-      for (int db = 0; db < C::kDB; ++db) {
-        const uint16_t* vrow = vs + (db * 32 + m) * C::kVStride + hh * 8;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const half8_t a = *reinterpret_cast<const half8_t*>(vrow + t * 16);
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[t], o[db], 0, 0, 0);
-        }
-      }
+      for (int g = 0; g < 4; ++g) ks[g] = ks_next[g];
     }
-    if (has_next) store_tile_lds<D>(smem + ((it + 1) & 1) * C::kStage, tid, kr, vr);
+    __syncthreads();
+  }
+  for (; kt < kv_end; kt += kBN, ++it) {
+    const bool has_next = kt + kBN < kv_end;
+    if (has_next) load_tile_regs<D>(p, kbase, vbase, ksp, kt + kBN, tid, kr, vr, ks_next);
+    if (!CAUSAL || kt <= wrow0 + 31) {  // a wave whose rows all precede kt skips the tile
+      attn_tile<D, CAUSAL, true>(p, smem + (it & 1) * C::kStage, qf, ks, qs, kt, qrow, m, hh, o, m_run, l_run);
+    }
+    if (has_next) {
+      store_tile_lds<D>(smem + ((it + 1) & 1) * C::kStage, tid, kr, vr);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) ks[g] = ks_next[g];
+    }
     __syncthreads();
   }
 
