@@ -119,6 +119,30 @@ def cpu_baseline(cfg, budget_s):
     }
 
 
+def kernels_only(cfg, q, k, v, n):
+    """Each kernel of the path n times, then a plain copy of 1 GiB n times (a
+    kernel of known traffic: FETCH_SIZE and WRITE_SIZE should read 1 GiB each)."""
+    import torch
+
+    from sageattention import ops
+
+    B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
+    lay = ops.HND if layout == "HND" else ops.NHD
+    for _ in range(n):
+        mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=q.device, dtype=q.dtype)
+        q8, qs, k8, ks = ops.quant_qk_int8(q, k, mean, lay, D ** -0.5)
+        vt = torch.empty(B, Hkv, D, (S + 63) // 64 * 64, device=q.device, dtype=torch.float16)
+        ops.v_transpose(v, vt, lay)
+        o = torch.empty_like(q)
+        ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5)
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=q.device)
+    dst = torch.empty_like(src)
+    for _ in range(n):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] kernels-only: {n} x path kernels + {n} x 1 GiB copy done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -127,6 +151,9 @@ def main():
     ap.add_argument("--config", default="NS", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="launch each path kernel --steps times plus a 1 GiB device copy (the HBM-counter "
+                         "calibration) and exit; for rocprofv3 --pmc runs")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -149,6 +176,9 @@ def main():
 
     q, k, v = make_inputs(cfg, dev)
     torch.cuda.synchronize()
+    if args.kernels_only:
+        kernels_only(cfg, q, k, v, args.steps)
+        return
 
     def step():
         return sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth)
