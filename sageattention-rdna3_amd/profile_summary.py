@@ -1,26 +1,117 @@
-"""Turn a rocprofv3 kernel-stats CSV into the markdown summary kept under profiles/.
+"""Summaries of rocprofv3 output kept under profiles/ (text only).
 
-Usage: python sageattention-rdna3_amd/profile_summary.py STATS_CSV OUT_MD "TITLE" "COMMAND"
+  python sageattention-rdna3_amd/profile_summary.py stats STATS_CSV OUT_MD TITLE COMMAND
+      kernel-trace statistics -> markdown table of this library's kernels
+  python sageattention-rdna3_amd/profile_summary.py traffic FETCH_CSV WRITE_CSV OUT_JSON OUT_MD COMMAND
+      two --pmc runs of `bench.py --kernels-only` (FETCH_SIZE, then WRITE_SIZE) -> HBM bytes per
+      launch of every path kernel, each counter scaled by what it reads for the 1 GiB device copy
+      the same run performs (a kernel of known traffic)
+  python sageattention-rdna3_amd/profile_summary.py counters OUT_MD COMMAND CSV [CSV ...]
+      --pmc runs -> per-kernel mean of every counter collected
 """
+import collections
 import csv
+import json
 import sys
 
+COPY_BYTES = 1 << 30
+KERNELS = ("attn_i8_fwd_kernel", "quant_qk_i8_kernel", "v_layout_kernel", "k_mean_partial_kernel",
+           "k_mean_final_kernel")
 
-def main():
-    stats, out, title, command = sys.argv[1:5]
-    rows = list(csv.DictReader(open(stats)))
+
+def short_name(name):
+    if "sage::" in name:
+        return name.split("(anonymous namespace)::")[1].split("(sage")[0]
+    if "copyBuffer" in name:
+        return "copy_1GiB"
+    return None
+
+
+def per_kernel(path, counter=None):
+    """{kernel: [value per dispatch]} summed over counter dimensions."""
+    acc = collections.defaultdict(float)
+    names = {}
+    for r in csv.DictReader(open(path)):
+        if counter and r["Counter_Name"] != counter:
+            continue
+        k = short_name(r["Kernel_Name"])
+        if k is None:
+            continue
+        key = (r["Dispatch_Id"], r["Counter_Name"])
+        acc[key] += float(r["Counter_Value"])
+        names[key] = k
+    out = collections.defaultdict(lambda: collections.defaultdict(list))
+    for key, v in acc.items():
+        out[names[key]][key[1]].append(v)
+    return out
+
+
+def stats(csv_path, out_md, title, command):
+    rows = list(csv.DictReader(open(csv_path)))
     lines = [f"# {title}", "", "Command (repo root on the GPU box):", "", f"    {command}", "",
              "Calls include bench.py's warmup, timed steps and its per-kernel HIP-event loops.", "",
              "| kernel | calls | avg (us) | min (us) | max (us) | share |", "|---|---|---|---|---|---|"]
     for r in rows:
-        name = r["Name"]
-        if "sage::" not in name:
+        k = short_name(r["Name"])
+        if k is None or k == "copy_1GiB":
             continue
-        short = name.split("(anonymous namespace)::")[1].split("(sage")[0]
-        lines.append(f"| `{short}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+        lines.append(f"| `{k}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                      f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {r['Percentage']}% |")
-    open(out, "w").write("\n".join(lines) + "\n")
+    open(out_md, "w").write("\n".join(lines) + "\n")
+
+
+def traffic(fetch_csv, write_csv, out_json, out_md, command):
+    fetch = per_kernel(fetch_csv, "FETCH_SIZE")
+    write = per_kernel(write_csv, "WRITE_SIZE")
+    mean = lambda d, k, c: sum(d[k][c]) / len(d[k][c]) * 1024.0  # KiB -> bytes
+    f_scale = COPY_BYTES / mean(fetch, "copy_1GiB", "FETCH_SIZE")
+    w_scale = COPY_BYTES / mean(write, "copy_1GiB", "WRITE_SIZE")
+    res = {"fetch_scale": f_scale, "write_scale": w_scale, "kernels": {}}
+    for k in fetch:
+        if k == "copy_1GiB" or k not in write:
+            continue
+        fb = mean(fetch, k, "FETCH_SIZE") * f_scale
+        wb = mean(write, k, "WRITE_SIZE") * w_scale
+        res["kernels"][k] = {"fetch_bytes": fb, "write_bytes": wb, "bytes": fb + wb}
+    attn = [v for k, v in res["kernels"].items() if k.startswith("attn_i8_fwd_kernel")]
+    if attn:
+        res["attn_bytes_per_launch"] = attn[0]["bytes"]
+    json.dump(res, open(out_json, "w"), indent=1)
+    lines = ["# HBM traffic per launch (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)", "",
+             "Commands (repo root on the GPU box), one counter per run:", ""]
+    lines += [f"    {c}" for c in command.split(" ;; ")]
+    lines += ["", f"Calibration with the 1 GiB device copy of the same runs: FETCH_SIZE x {f_scale:.3f}, "
+              f"WRITE_SIZE x {w_scale:.3f}.", "",
+              "| kernel | fetch (MB) | write (MB) | total (MB) |", "|---|---|---|---|"]
+    for k, v in res["kernels"].items():
+        lines.append(f"| `{k}` | {v['fetch_bytes'] / 1e6:.1f} | {v['write_bytes'] / 1e6:.1f} | {v['bytes'] / 1e6:.1f} |")
+    open(out_md, "w").write("\n".join(lines) + "\n")
+
+
+def counters(out_md, command, paths):
+    merged = collections.defaultdict(dict)
+    for pth in paths:
+        for k, cs in per_kernel(pth).items():
+            for c, vals in cs.items():
+                merged[k][c] = sum(vals) / len(vals)
+    lines = ["# rocprofv3 --pmc counters per kernel (mean over dispatches, summed over dimensions)", "",
+             "Commands (repo root on the GPU box), one counter group per run:", ""]
+    lines += [f"    {c}" for c in command.split(" ;; ")]
+    lines += [""]
+    for k in sorted(merged):
+        lines += [f"## `{k}`", "", "| counter | value |", "|---|---|"]
+        lines += [f"| {c} | {v:.4g} |" for c, v in sorted(merged[k].items())]
+        lines += [""]
+    open(out_md, "w").write("\n".join(lines) + "\n")
 
 
 if __name__ == "__main__":
-    main()
+    mode = sys.argv[1]
+    if mode == "stats":
+        stats(*sys.argv[2:6])
+    elif mode == "traffic":
+        traffic(*sys.argv[2:7])
+    elif mode == "counters":
+        counters(sys.argv[2], sys.argv[3], sys.argv[4:])
+    else:
+        raise SystemExit(__doc__)
