@@ -15,24 +15,29 @@
 //     softmax is 32 in-lane values plus one permlane32 swap;
 //   * O^T = V^T . P^T with v_mfma_f32_32x32x16_f16: B = P^T taken straight
 //     from the S^T accumulators (no LDS round trip), A = V_T rows from LDS.
-//     The k-order of P inside each 16-key step is (4h..4h+3, 8+4h..8+4h+3)
-//     for lane half h; V_T tiles are stored in LDS with bits 2 and 3 of the
-//     key index swapped so each lane reads its 8 keys as one 16-byte load;
-//   * ping-pong: waves 0-3 and 4-7 (one of each per SIMD) run a phase apart.
-//     Each tile takes two barrier-separated phases; in every phase one wave
-//     of a SIMD issues only MFMAs (S of tile j and P.V of tile j-1) while the
-//     other runs only the VALU softmax of its tile, so the matrix cores and
-//     the VALU of each SIMD stay busy at the same time;
-//   * online softmax with a lazy reference max: O and l are rescaled only when
-//     a row max grows by more than 2^8, so most tiles touch O only in MFMAs;
-//   * K/V tiles are double buffered in LDS; global loads go through buffer
-//     descriptors (tail rows of K read as zero) one phase ahead of the store;
-//   * causal: the KV loop stops at the block's last row, waves skip tiles
-//     left of their rows' reach, masks only on tail / diagonal tiles;
+//     K rows sit in LDS with bits 2 and 3 of the key index swapped, which
+//     makes accumulator register r of lane half h hold key 16(r/8) + 8h + r%8:
+//     exactly the 8 consecutive keys the PV operand wants from that lane;
+//   * software pipeline inside every wave: step j runs the softmax of tile j
+//     (VALU) interleaved with the MFMAs of P_{j-1}.V_{j-1} and S_{j+1} =
+//     K_{j+1}.Q^T, so each wave keeps the matrix core and the VALU busy at
+//     once and the two waves of a SIMD fill each other's gaps.  A single wave
+//     issues VALU at half the SIMD's rate, so both waves of a SIMD carry
+//     softmax work all the time (no MFMA-only / VALU-only roles).  S and P are
+//     rewritten in place: the chunk order reads each before overwriting it;
+//   * online softmax with a lazy reference max: the max moves only when a row
+//     max grows by more than 2^8; O is then rescaled at the top of the next
+//     step, after the P.V MFMAs that still used the old max;
+//   * K/V tiles stream into a 3-stage LDS ring with buffer_load ... lds
+//     (no staging registers), issued two steps ahead; loads past the block's
+//     last key read as zero through the descriptor's record count;
+//   * causal: the KV loop stops at the block's last row, masks only on tail /
+//     diagonal tiles;
 //   * block -> work remap keeps consecutive q-blocks of a head on one XCD
 //     (shared L2 for K/V) and issues the heaviest causal blocks first.
 #include <cmath>
 #include <type_traits>
+#include <utility>
 
 #include "sage_common.h"
 
@@ -65,19 +70,44 @@ struct AttnParams {
 
 template <int D>
 struct Cfg {
-  static constexpr int kKStride = D + 16;                    // bytes per K row in LDS
-  static constexpr int kVStride = kBN + 8;                   // halves per V_T row in LDS
-  static constexpr int kKStage = kBN * kKStride;             // bytes of one K stage
-  static constexpr int kVStage = D * kVStride * 2;           // bytes of one V stage
-  static constexpr int kVBase = 2 * kKStage;                 // V stages follow the two K stages
-  static constexpr int kSmem = 2 * kKStage + 2 * kVStage;
-  static constexpr int kKTasks = kBN * D / 16;               // 16-byte K chunks per tile
-  static constexpr int kVTasks = D * kBN / 8;                // 16-byte V_T chunks per tile
-  static constexpr int kKChunks = (kKTasks + kThreads - 1) / kThreads;
-  static constexpr int kVChunks = (kVTasks + kThreads - 1) / kThreads;
+  static constexpr int kStages = 3;                          // LDS ring depth (K and V)
+  static constexpr int kKRow = D;                            // bytes per K row in LDS (unpadded)
+  static constexpr int kVRow = kBN * 2;                      // bytes per V_T row in LDS (unpadded)
+  static constexpr int kKStage = kBN * kKRow;                // bytes of one K stage
+  static constexpr int kVStage = D * kVRow;                  // bytes of one V stage
+  static constexpr int kKBase = kStages * kVStage;           // K stages follow the V stages
+  static constexpr int kSmem = kStages * (kKStage + kVStage);
+  static constexpr int kKLoads = kKStage / 1024;             // 1 KB LDS-direct loads per K tile
+  static constexpr int kVLoads = kVStage / 1024;             // ... per V tile
+  static constexpr int kVPerWave = kVLoads / kWaves;
+  // loads every wave issues per step (waves 0..kKLoads-1 issue one more when
+  // a K tile has fewer 1 KB pieces than there are waves); waiting until at
+  // most this many are in flight retires everything issued a step earlier
+  static constexpr int kStepLoads = kVPerWave + (kKLoads >= kWaves ? 1 : 0);
   static constexpr int kDS = D / 32;                         // k-steps of the QK MFMA
   static constexpr int kDB = D / 32;                         // 32-row d blocks of O^T
+  static_assert(kVLoads % kWaves == 0, "V tile must split evenly over the waves");
+  static_assert(kKLoads == kWaves || kKLoads < kWaves, "at most one K piece per wave");
 };
+
+// LDS tiles are unpadded rows of 16-byte chunks; chunk c of row r is stored at
+// chunk position c ^ swz(r).  gfx950's LDS serves 256 bytes (64 banks) per
+// cycle, i.e. 16 lanes of a ds_read_b128; the 16 lanes of an MFMA operand read
+// take one chunk each from 16 consecutive rows.  Rows r and r + 256/ROW_BYTES
+// share banks, so the XOR key is the row's index among those: every 16-lane
+// group then covers all 64 banks once.  The XOR is its own inverse, so the
+// same function maps position -> chunk for the loads.
+template <int ROW_BYTES>
+__device__ __forceinline__ int swz(int row) {
+  static_assert(ROW_BYTES == 128 || ROW_BYTES == 64, "rows of 4 or 8 chunks");
+  constexpr int kRowsPerWindow = 256 / ROW_BYTES;
+  constexpr int kChunks = ROW_BYTES / 16;
+  return (row / kRowsPerWindow) & (kChunks - 1);
+}
+
+// LDS row r of a K stage holds key kperm(r) of the tile (bits 2 and 3 swapped;
+// an involution).
+__device__ __forceinline__ int kperm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -110,82 +140,74 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            static_cast<int>(__builtin_amdgcn_readfirstlane(bytes)), kBufferWord3);
 }
 
-// Tile copy global -> registers -> LDS, shared by all threads of the block.
-// Chunk i of a thread lies i passes after chunk 0 (a pass = kThreads chunks),
-// so only chunk 0's offsets live in registers: later chunks add a
-// compile-time LDS delta and a uniform global delta.
+// One 16-byte-per-lane buffer load straight into LDS (buffer_load_dwordx4
+// ... lds): the wave's 64 lanes fill 1 KB at `lds_dst` + lane*16; lanes whose
+// offset lies past the descriptor's end write zeros.  The builtin takes an
+// LDS-address-space pointer, which only the device pass of this single-source
+// file can form; in the host pass (which compiles no device code but would
+// otherwise drop the kernels' launch stubs) the body is empty.
+__device__ __forceinline__ void lds_direct_load16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  // the low 32 bits of a generic LDS address are the LDS offset
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, reinterpret_cast<lds_ptr>(reinterpret_cast<uintptr_t>(lds_dst)), 16,
+                                           voffset, 0, 0, 0);
+#endif
+}
+
+// Tile loads straight from global memory into LDS.  Each wave instruction
+// fills 1 KB of LDS at M0 + lane*16, so a lane's source address picks the
+// chunk that belongs at its LDS position (inverse swizzle; K rows also go
+// through kperm).  Descriptors end at the block's last key (kv_end), so tiles
+// past it, and K rows past it, read as zero without touching memory.
 template <int D>
-struct TileCopy {
+struct TileLoader {
   using C = Cfg<D>;
-  static constexpr int kKRowsPerPass = kThreads / (D / 16);   // K rows per pass
-  static constexpr int kVRowsPerPass = kThreads / (kBN / 8);  // V_T d-rows per pass
-  uint32_t k_goff, k_loff, v_goff, v_loff;
-  uint4 kr[C::kKChunks];
-  uint4 vr[C::kVChunks];
+  uint32_t k_goff;                 // this lane's byte offset in the K tile
+  uint32_t v_goff[C::kVPerWave];   // ... in the V_T tile (row pitch np)
+  bool k_wave;                     // this wave loads one 1 KB piece of K
 
-  __device__ __forceinline__ TileCopy(int tid, int np) {
-    const int row = tid / (D / 16);
-    const int c16 = tid % (D / 16);
-    k_goff = row * D + c16 * 16;
-    k_loff = row * C::kKStride + c16 * 16;
-    const int d = tid / (kBN / 8);
-    const int n8 = tid % (kBN / 8);
-    v_goff = static_cast<uint32_t>((d * np + n8 * 8) * 2);
-    // keys n8*8 .. n8*8+7 of row d: within their 16-key group, keys with
-    // bit3 = n8&1 and bit2 = 0 / 1 go to positions (n8&1)*4 / 8 + (n8&1)*4
-    v_loff = (d * C::kVStride + (n8 >> 1) * 16 + (n8 & 1) * 4) * 2;
-  }
-
-  // K rows kt.. (rows >= sk read as zero) and V_T tokens kt.. (always inside
-  // the padded row) into registers.
-  __device__ __forceinline__ void load(const AttnParams& p, const int8_t* kbase, const uint16_t* vbase, int kt,
-                                       bool do_k, bool do_v, int tid) {
-    if (do_k) {
-      const int rows = min(p.sk - kt, kBN);
-      const auto rk = make_rsrc(kbase + static_cast<int64_t>(kt) * D, static_cast<uint32_t>(max(rows, 0) * D));
-#pragma unroll
-      for (int i = 0; i < C::kKChunks; ++i) {
-        if (C::kKTasks % kThreads == 0 || tid + i * kThreads < C::kKTasks) {
-          const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(rk, k_goff + i * kKRowsPerPass * D, 0, 0);
-          kr[i] = make_uint4(w.x, w.y, w.z, w.w);
-        }
-      }
+  __device__ __forceinline__ TileLoader(int wave, int lane, int np) {
+    k_wave = wave < C::kKLoads;
+    {
+      const int byte = wave * 1024 + lane * 16;  // LDS byte in the K stage
+      const int row = byte / C::kKRow;
+      const int c = ((byte % C::kKRow) / 16) ^ swz<C::kKRow>(row);
+      k_goff = kperm(row) * D + c * 16;
     }
-    if (do_v) {
-      const auto rv = make_rsrc(vbase + kt, static_cast<uint32_t>((D * static_cast<int>(p.np) - kt) * 2));
-      const int pass = __builtin_amdgcn_readfirstlane(kVRowsPerPass * static_cast<int>(p.np) * 2);
 #pragma unroll
-      for (int i = 0; i < C::kVChunks; ++i) {
-        if (C::kVTasks % kThreads == 0 || tid + i * kThreads < C::kVTasks) {
-          const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(rv, v_goff, i * pass, 0);
-          vr[i] = make_uint4(w.x, w.y, w.z, w.w);
-        }
-      }
+    for (int i = 0; i < C::kVPerWave; ++i) {
+      const int byte = (wave * C::kVPerWave + i) * 1024 + lane * 16;
+      const int row = byte / C::kVRow;
+      const int c = ((byte % C::kVRow) / 16) ^ swz<C::kVRow>(row);
+      v_goff[i] = static_cast<uint32_t>(row * np * 2 + c * 16);
     }
   }
 
-  __device__ __forceinline__ void store(char* smem, int stage, bool do_k, bool do_v, int tid) {
-    if (do_k) {
-      char* kb = smem + stage * C::kKStage + k_loff;
-#pragma unroll
-      for (int i = 0; i < C::kKChunks; ++i) {
-        if (C::kKTasks % kThreads == 0 || tid + i * kThreads < C::kKTasks)
-          *reinterpret_cast<uint4*>(kb + i * kKRowsPerPass * C::kKStride) = kr[i];
-      }
+  __device__ __forceinline__ void issue_k(const int8_t* kbase, char* kstage, int kt, int kv_end, int wave) const {
+    if (k_wave) {
+      const int rows = min(max(kv_end - kt, 0), kBN);
+      const auto rk = make_rsrc(kbase + static_cast<int64_t>(min(kt, kv_end)) * D, static_cast<uint32_t>(rows * D));
+      lds_direct_load16(rk, kstage + wave * 1024, k_goff);
     }
-    if (do_v) {
-      char* vb = smem + C::kVBase + stage * C::kVStage + v_loff;
+  }
+  __device__ __forceinline__ void issue_v(const AttnParams& p, const uint16_t* vbase, char* vstage, int kt, int kv_end,
+                                          int wave) const {
+    const bool live = kt >= 0 && kt < kv_end;
+    const int kc = live ? kt : 0;
+    const auto rv = make_rsrc(vbase + kc, live ? static_cast<uint32_t>((D * static_cast<int>(p.np) - kc) * 2) : 0u);
 #pragma unroll
-      for (int i = 0; i < C::kVChunks; ++i) {
-        if (C::kVTasks % kThreads == 0 || tid + i * kThreads < C::kVTasks) {
-          char* dst = vb + i * kVRowsPerPass * C::kVStride * 2;
-          *reinterpret_cast<uint2*>(dst) = make_uint2(vr[i].x, vr[i].y);
-          *reinterpret_cast<uint2*>(dst + 16) = make_uint2(vr[i].z, vr[i].w);
-        }
-      }
-    }
+    for (int i = 0; i < C::kVPerWave; ++i) lds_direct_load16(rv, vstage + (wave * C::kVPerWave + i) * 1024, v_goff[i]);
   }
 };
+
+// Wait until at most N LDS-direct loads of this wave are in flight, then a
+// workgroup barrier.  One asm statement: the compiler neither moves LDS
+// accesses across it nor adds its own vmcnt(0) (which __syncthreads would).
+template <int N>
+__device__ __forceinline__ void wait_loads_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 // The tile's 4 key-group scales, read through the constant address space so
 // they land in SGPRs (the address is wave-uniform and nothing writes the
@@ -201,132 +223,268 @@ __device__ __forceinline__ void load_ks(const AttnParams& p, const float* ksp, i
   }
 }
 
-// S^T of one 64-key tile for the wave's 32 queries: two 32x32 int32 blocks.
+// Per-lane LDS byte offsets of the MFMA operand reads: lane (m, hh) reads
+// 16-byte chunk 2x+hh (x = k-step) of row m; blocks of 32 more rows keep the
+// same swizzle (32 is a multiple of the swizzle period).  The K offsets carry
+// the K ring's base, so that stage and block offsets (< 64 KB) fold into the
+// ds_read immediate.
 template <int D>
-__device__ __forceinline__ void qk_tile(const char* kstage, const int4_t (&qf)[Cfg<D>::kDS], int m, int hh,
+struct OperandMap {
+  using C = Cfg<D>;
+  uint32_t k_off[C::kDS];
+  uint32_t v_off[4];
+  __device__ __forceinline__ OperandMap(int m, int hh) {
+#pragma unroll
+    for (int x = 0; x < C::kDS; ++x)
+      k_off[x] = C::kKBase + m * C::kKRow + (((2 * x + hh) ^ swz<C::kKRow>(m)) * 16);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) v_off[x] = m * C::kVRow + (((2 * x + hh) ^ swz<C::kVRow>(m)) * 16);
+  }
+};
+
+// Softmax of one tile for one wave, cut into pieces that the pipelined step
+// spreads between its MFMAs: S (int32 accumulators, read only) -> P (fp16
+// fragments), running max and sum.  O is not touched: when the reference max
+// moves (need), alpha = exp2(m_old - m_new) is left for the caller to apply to
+// O before the next P.V.  On masked tiles the dead keys (j >= Sk, causal
+// j > i) are re-derived where they are used instead of being written into a
+// copy of S (register budget).  The 32 probabilities go in 16 pairs i (16-key
+// step t = i/4, registers 8(t%2) + 2(i%4) .. +1 of block t/2), each in three
+// stages that the step places in consecutive chunks, so the exp latency of one
+// pair hides behind the work of its neighbours:
+//   pieces 0-3     integer max of key group g, scaled (group g = step g)
+//   piece  4       row max, lazy reference max, alpha
+//   pieces 5-20    A(i): y = acc*sc - m_run (dequant and max in one FMA)
+//   pieces 21-36   B(i): e = exp2(y)
+//   pieces 37-52   C(i): fp16 RNE pair into the P^T fragment, partial sums
+//   piece  53      l = l*alpha + sums
+template <int D, bool CAUSAL, bool MASK>
+struct TileSoftmax {
+  static constexpr int kPieces = 54;
+  const AttnParams& p;
+  const int16_t_ (&acc)[2];
+  const float (&ks)[4];
+  float qs;
+  int kt, qrow, hh;
+  float sc[4];
+  float gv[4];
+  float y[16][2];
+  float e[16][2];
+  float lsum[2];
+  uint32_t w[4][4];
+
+  __device__ __forceinline__ TileSoftmax(const AttnParams& p_, const int16_t_ (&acc_)[2], const float (&ks_)[4],
+                                         float qs_, int kt_, int qrow_, int hh_)
+      : p(p_), acc(acc_), ks(ks_), qs(qs_), kt(kt_), qrow(qrow_), hh(hh_) {
+    lsum[0] = lsum[1] = 0.0f;
+  }
+
+  // register r of block nb holds key kt + 32 nb + 16 (r/8) + 8 hh + r%8
+  __device__ __forceinline__ bool dead(int nb, int r) const {
+    const int n = kt + nb * 32 + 16 * (r >> 3) + 8 * hh + (r & 7);
+    return (n >= p.sk) || (CAUSAL && n > qrow);
+  }
+
+  template <int K>
+  __device__ __forceinline__ void piece(float& m_run, float& l_run, float& alpha, bool& need, half8_t (&pf)[4]) {
+    if constexpr (K < 4) {
+      // dequant scale fl(q_scale * k_scale) and the group's integer max: x ->
+      // x*sc is monotonic for sc > 0, so this is max_j fl(acc*sc); dead keys
+      // count as INT32_MIN, which no real dot product reaches (|acc| <=
+      // 128*128*D < 2^22)
+      constexpr int g = K, nb = g >> 1;
+      sc[g] = qs * ks[g];
+      int gm = INT32_MIN;
+#pragma unroll
+      for (int r = (g & 1) * 8; r < (g & 1) * 8 + 8; ++r) {
+        int a = acc[nb][r];
+        if constexpr (MASK) a = dead(nb, r) ? INT32_MIN : a;
+        gm = max(gm, a);
+      }
+      gv[g] = static_cast<float>(gm) * sc[g];
+      if constexpr (MASK) gv[g] = (gm == INT32_MIN) ? -INFINITY : gv[g];
+    } else if constexpr (K == 4) {
+      // lazy reference max: it moves only when some row's max grew by more
+      // than kRescale (log2 units), so p = exp2(s - m_run) stays below
+      // 2^kRescale (no fp16 overflow).  A row with no live key yet keeps -inf
+      // unless the wave moves, and then takes 0 (alpha = 0; its O and l are 0).
+      const float mx = xhalf_max(__builtin_fmaxf(__builtin_fmaxf(gv[0], gv[1]), __builtin_fmaxf(gv[2], gv[3])));
+      need = __builtin_amdgcn_ballot_w64(mx > m_run + kRescale) != 0;
+      float m_new = __builtin_fmaxf(m_run, mx);
+      m_new = (m_new == -INFINITY) ? 0.0f : m_new;
+      m_new = need ? m_new : m_run;
+      alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
+      m_run = m_new;
+    } else if constexpr (K < 21) {
+      constexpr int i = K - 5, t = i >> 2, nb = t >> 1, r0 = (t & 1) * 8 + 2 * (i & 3);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) y[i][u] = __builtin_fmaf(static_cast<float>(acc[nb][r0 + u]), sc[t], -m_run);
+    } else if constexpr (K < 37) {
+      constexpr int i = K - 21, t = i >> 2, nb = t >> 1, r0 = (t & 1) * 8 + 2 * (i & 3);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        e[i][u] = fast_exp2(y[i][u]);
+        if constexpr (MASK) e[i][u] = dead(nb, r0 + u) ? 0.0f : e[i][u];
+      }
+    } else if constexpr (K < 53) {
+      constexpr int i = K - 37, t = i >> 2, j = i & 3;
+      lsum[0] += e[i][0];
+      lsum[1] += e[i][1];
+      w[t][j] = pack_f16x2(e[i][0], e[i][1]);
+      if constexpr (j == 3) pf[t] = __builtin_bit_cast(half8_t, make_uint4(w[t][0], w[t][1], w[t][2], w[t][3]));
+    } else if constexpr (K == 53) {
+      l_run = __builtin_fmaf(l_run, alpha, lsum[0] + lsum[1]);
+    }
+  }
+};
+
+// The MFMAs of one pipelined step in issue order: the P.V MFMAs of the
+// previous tile (16-key step t major, the d blocks' accumulation chains
+// alternate; lane half h supplies keys 16t + 8h .. 16t + 8h + 7), then the
+// QK MFMAs of the next tile, key block 0 before key block 1.  MFMA i reads its
+// A operand (16 bytes per lane) from LDS kAhead MFMAs earlier.
+template <int D>
+struct StepMfma {
+  using C = Cfg<D>;
+  static constexpr int kPV = 4 * C::kDB;
+  static constexpr int kQK = 2 * C::kDS;
+  static constexpr int kN = kPV + kQK;
+  static constexpr int kAhead = 2;
+  const char* vst;
+  const char* kst;
+  const OperandMap<D>& om;
+  int4_t ring[kAhead + 1];
+
+  __device__ __forceinline__ StepMfma(const char* vst_, const char* kst_, const OperandMap<D>& om_)
+      : vst(vst_), kst(kst_), om(om_) {}
+
+  template <int I>
+  __device__ __forceinline__ void read() {
+    if constexpr (I < kPV) {
+      constexpr int t = I / C::kDB, db = I % C::kDB;
+      ring[I % (kAhead + 1)] = *reinterpret_cast<const int4_t*>(vst + db * 32 * C::kVRow + om.v_off[t]);
+    } else if constexpr (I < kN) {
+      constexpr int q = I - kPV, nb = q / C::kDS, ds = q % C::kDS;
+      ring[I % (kAhead + 1)] = *reinterpret_cast<const int4_t*>(kst + nb * 32 * C::kKRow + om.k_off[ds]);
+    }
+  }
+  template <int I>
+  __device__ __forceinline__ void mfma(const half8_t (&pf)[4], float16_t_ (&o)[C::kDB], const int4_t (&qf)[C::kDS],
+                                       int16_t_ (&acc)[2]) {
+    if constexpr (I < kPV) {
+      constexpr int t = I / C::kDB, db = I % C::kDB;
+      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, ring[I % (kAhead + 1)]), pf[t], o[db],
+                                                     0, 0, 0);
+    } else {
+      constexpr int q = I - kPV, nb = q / C::kDS, ds = q % C::kDS;
+      acc[nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[I % (kAhead + 1)], qf[ds], ds == 0 ? int16_t_{} : acc[nb],
+                                                      0, 0, 0);
+    }
+  }
+};
+
+
+// Softmax pieces of chunk c of a step (k-th of at most kMaxPieces; -1 =
+// none).  S and P are updated in place, so the order must respect: P^T
+// fragment t is rewritten (stage C of pairs 4t..4t+3) only after the P.V MFMAs
+// that read it, and key block nb of S is read (group maxima, stage A) for the
+// last time before the first QK MFMA that overwrites it.  Stage A of pair i
+// needs the reference max of piece 4 (one chunk of slack for its ballot).
+constexpr int kMaxPieces = 6;
+template <int D>
+constexpr int chunk_piece(int c, int k) {
+  int list[kMaxPieces] = {-1, -1, -1, -1, -1, -1};
+  int n = 0;
+  if constexpr (D == 128) {
+    // 24 MFMAs: P.V step t at 4t..4t+3, QK block 0 at 16-19, block 1 at 20-23;
+    // pair i: A in chunk i+4, B in i+5, C in i+6
+    if (c == 0) { list[n++] = 0; list[n++] = 1; }
+    if (c == 1) { list[n++] = 2; list[n++] = 3; }
+    if (c == 2) list[n++] = 4;
+    if (c - 6 >= 0 && c - 6 < 16) list[n++] = 37 + c - 6;
+    if (c - 5 >= 0 && c - 5 < 16) list[n++] = 21 + c - 5;
+    if (c - 4 >= 0 && c - 4 < 16) list[n++] = 5 + c - 4;
+    if (c == 22) list[n++] = 53;
+  } else {
+    // 12 MFMAs: P.V step t at 2t, 2t+1, QK block 0 at 8-9, block 1 at 10-11;
+    // pairs 2q, 2q+1: A in chunk q+2, B in q+3, C in q+4
+    if (c == 0) { list[n++] = 0; list[n++] = 1; list[n++] = 2; list[n++] = 3; }
+    if (c == 1) list[n++] = 4;
+    for (int u = 0; u < 2; ++u) {
+      if (c - 4 >= 0 && c - 4 < 8) list[n++] = 37 + 2 * (c - 4) + u;
+      if (c - 3 >= 0 && c - 3 < 8) list[n++] = 21 + 2 * (c - 3) + u;
+      if (c - 2 >= 0 && c - 2 < 8) list[n++] = 5 + 2 * (c - 2) + u;
+    }
+    if (c == 11) list[n++] = 53;
+  }
+  return k < n ? list[k] : -1;
+}
+
+template <typename SM, int... K>
+__device__ __forceinline__ void run_all_pieces(SM& sm, std::integer_sequence<int, K...>, float& m_run, float& l_run,
+                                               float& alpha, bool& need, half8_t (&pf)[4]) {
+  (sm.template piece<K>(m_run, l_run, alpha, need, pf), ...);
+}
+template <typename SM, int K>
+__device__ __forceinline__ void run_piece(SM& sm, float& m_run, float& l_run, float& alpha, bool& need,
+                                          half8_t (&pf)[4]) {
+  if constexpr (K >= 0) sm.template piece<K>(m_run, l_run, alpha, need, pf);
+}
+
+// One pipelined step: MFMA i, the operand read of MFMA i + kAhead and the
+// softmax pieces of chunk i, one chunk per MFMA; sched_barrier keeps the
+// chunks in this order, so the wave issues VALU work while each MFMA runs.
+template <int D, typename SM, int I>
+__device__ __forceinline__ void step_chunk(StepMfma<D>& mf, SM& sm, const half8_t (&p_prv)[4],
+                                           float16_t_ (&o)[Cfg<D>::kDB], const int4_t (&qf)[Cfg<D>::kDS],
+                                           int16_t_ (&s_nxt)[2], float& m_run, float& l_run, float& alpha, bool& need,
+                                           half8_t (&p_cur)[4]) {
+  mf.template read<I + StepMfma<D>::kAhead>();
+  mf.template mfma<I>(p_prv, o, qf, s_nxt);
+  run_piece<SM, chunk_piece<D>(I, 0)>(sm, m_run, l_run, alpha, need, p_cur);
+  run_piece<SM, chunk_piece<D>(I, 1)>(sm, m_run, l_run, alpha, need, p_cur);
+  run_piece<SM, chunk_piece<D>(I, 2)>(sm, m_run, l_run, alpha, need, p_cur);
+  run_piece<SM, chunk_piece<D>(I, 3)>(sm, m_run, l_run, alpha, need, p_cur);
+  run_piece<SM, chunk_piece<D>(I, 4)>(sm, m_run, l_run, alpha, need, p_cur);
+  run_piece<SM, chunk_piece<D>(I, 5)>(sm, m_run, l_run, alpha, need, p_cur);
+  __builtin_amdgcn_sched_barrier(0);
+}
+template <int D, typename SM, int... I>
+__device__ __forceinline__ void step_chunks(std::integer_sequence<int, I...>, StepMfma<D>& mf, SM& sm,
+                                            const half8_t (&p_prv)[4], float16_t_ (&o)[Cfg<D>::kDB],
+                                            const int4_t (&qf)[Cfg<D>::kDS], int16_t_ (&s_nxt)[2], float& m_run,
+                                            float& l_run, float& alpha, bool& need, half8_t (&p_cur)[4]) {
+  (step_chunk<D, SM, I>(mf, sm, p_prv, o, qf, s_nxt, m_run, l_run, alpha, need, p_cur), ...);
+}
+
+// S^T of one 64-key tile for the wave's 32 queries (prologue only).
+template <int D>
+__device__ __forceinline__ void qk_tile(const char* kstage, const OperandMap<D>& om, const int4_t (&qf)[Cfg<D>::kDS],
                                         int16_t_ (&acc)[2]) {
   using C = Cfg<D>;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const char* krow = kstage + (nb * 32 + m) * C::kKStride + hh * 16;
+  for (int ds = 0; ds < C::kDS; ++ds) {
 #pragma unroll
-    for (int ds = 0; ds < C::kDS; ++ds) {
-      const int4_t a = *reinterpret_cast<const int4_t*>(krow + ds * 32);
+    for (int nb = 0; nb < 2; ++nb) {
+      const int4_t a = *reinterpret_cast<const int4_t*>(kstage + nb * 32 * C::kKRow + om.k_off[ds]);
       acc[nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[ds], ds == 0 ? int16_t_{} : acc[nb], 0, 0, 0);
     }
   }
-  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-  for (int i = 0; i < 2 * C::kDS - 2; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 }
 
-// O^T += V^T . P^T for one 64-key tile.
+// O^T += V^T . P^T for one 64-key tile (the last tile only).
 template <int D>
-__device__ __forceinline__ void pv_tile(const char* vstage, const half8_t (&pf)[4], int m, int hh,
+__device__ __forceinline__ void pv_tile(const char* vstage, const OperandMap<D>& om, const half8_t (&pf)[4],
                                         float16_t_ (&o)[Cfg<D>::kDB]) {
   using C = Cfg<D>;
-  const uint16_t* vs = reinterpret_cast<const uint16_t*>(vstage);
 #pragma unroll
-  for (int db = 0; db < C::kDB; ++db) {
-    const uint16_t* vrow = vs + (db * 32 + m) * C::kVStride + hh * 8;
+  for (int t = 0; t < 4; ++t) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const half8_t a = *reinterpret_cast<const half8_t*>(vrow + t * 16);
+    for (int db = 0; db < C::kDB; ++db) {
+      const half8_t a = *reinterpret_cast<const half8_t*>(vstage + db * 32 * C::kVRow + om.v_off[t]);
       o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[t], o[db], 0, 0, 0);
     }
   }
-  // operands read two MFMAs ahead of use, not all at once (register budget)
-  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-  for (int i = 0; i < 4 * C::kDB - 2; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-}
-
-// Softmax of one tile for one wave: S (int32 in `acc`, read only) -> P (fp16
-// fragments in `pf`), updating the running max / sum and, rarely, rescaling O.
-// On masked tiles the dead keys (j >= Sk, causal j > i) are re-derived where
-// they are used instead of being written into a copy of S (register budget).
-template <int D, bool CAUSAL, bool MASK>
-__device__ __forceinline__ void softmax_tile(const AttnParams& p, const int16_t_ (&acc)[2], const float (&ks)[4],
-                                             float qs, int kt, int qrow, int hh, half8_t (&pf)[4],
-                                             float16_t_ (&o)[Cfg<D>::kDB], float& m_run, float& l_run) {
-  using C = Cfg<D>;
-  auto dead = [&](int nb, int r) {
-    const int n = kt + nb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-    return (n >= p.sk) || (CAUSAL && n > qrow);
-  };
-  // ---- dequant scales of the 4 key groups: fl(q_scale * k_scale)
-  float sc[4];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) sc[g] = qs * ks[g];
-  // ---- row max: integer max inside each 16-key group, then one scale per
-  // group (x -> x*sc is monotonic for sc > 0, so this is max_j fl(acc*sc));
-  // dead keys count as INT32_MIN, which no real dot product reaches
-  // (|acc| <= 128*128*D < 2^22)
-  float mx = -INFINITY;
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int nb = g >> 1;
-    int gm = INT32_MIN;
-#pragma unroll
-    for (int r = (g & 1) * 8; r < (g & 1) * 8 + 8; ++r) {
-      int a = acc[nb][r];
-      if constexpr (MASK) a = dead(nb, r) ? INT32_MIN : a;
-      gm = max(gm, a);
-    }
-    float gv = static_cast<float>(gm) * sc[g];
-    if constexpr (MASK) gv = (gm == INT32_MIN) ? -INFINITY : gv;
-    mx = __builtin_fmaxf(mx, gv);
-  }
-  mx = xhalf_max(mx);
-  // ---- lazy rescale: the reference max only moves when some row's max grew
-  // by more than kRescale (log2 units), so p = exp2(s - m_run) stays below
-  // 2^kRescale (no fp16 overflow) and O is rescaled only on those tiles.
-  if (__builtin_amdgcn_ballot_w64(mx > m_run + kRescale) != 0) {
-    // keeps the block a real branch: without it the 64 multiplies of O are
-    // speculated onto every tile (they are only 4 vector ops in the IR)
-    asm volatile("" ::: "memory");
-    float m_new = __builtin_fmaxf(m_run, mx);
-    m_new = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
-#pragma unroll
-    for (int db = 0; db < C::kDB; ++db) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-    }
-  }
-  // ---- p = exp2(acc*sc - m_run): dequant and max subtraction in one FMA;
-  // P^T fragments (fp16 RNE) straight from the accumulator layout
-  float lsum = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    uint32_t w[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float e2[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int nb = t >> 1;
-        const int r = (t & 1) * 8 + 2 * j + u;
-        float e = fast_exp2(__builtin_fmaf(static_cast<float>(acc[nb][r]), sc[t], -m_run));
-        if constexpr (MASK) e = dead(nb, r) ? 0.0f : e;
-        lsum += e;
-        e2[u] = e;
-      }
-      w[j] = pack_f16x2(e2[0], e2[1]);
-    }
-    pf[t] = __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
-  }
-  l_run += lsum;
 }
 
 template <int D, bool CAUSAL, bool OUT_BF16>
@@ -350,7 +508,6 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int role = wave >> 2;  // 0: MFMA phase first; 1: a phase behind
   const int lane = tid & 63;
   const int m = lane & 31;
   const int hh = lane >> 5;
@@ -379,9 +536,9 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
 
   const int kv_end = CAUSAL ? min(q0 + kBM, p.sk) : p.sk;
   const int ntiles = (kv_end + kBN - 1) / kBN;
-  // tiles [0, w_main) need no mask for this wave (inside the key range and,
-  // causal, left of the wave's first row)
-  const int w_main = CAUSAL ? min(wrow0 + 1, p.sk) / kBN : p.sk / kBN;
+  // tiles [0, n_main) need no mask for any wave of the block (inside the key
+  // range and, causal, left of the block's first row)
+  const int n_main = min(CAUSAL ? min(q0, p.sk) / kBN : p.sk / kBN, ntiles);
 
   float16_t_ o[C::kDB];
 #pragma unroll
@@ -391,89 +548,115 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   }
   float m_run = -INFINITY;
   float l_run = 0.0f;
-  int16_t_ acc[2];
-  half8_t pf[4];
+  float alpha = 1.0f;
+  bool need = false;
+  int16_t_ s[2];     // S of the tile the next softmax reads
+  half8_t pf[4];     // P^T fragments of the tile the next P.V reads
+#pragma unroll
+  for (int t = 0; t < 4; ++t) pf[t] = half8_t{};
   float ks[4];
 
-  TileCopy<D> tc(tid, static_cast<int>(p.np));
-  // ---- prologue: K_0 into stage 0
-  if (ntiles > 0) {
-    tc.load(p, kbase, vbase, 0, true, false, tid);
-    tc.store(smem, 0, true, false, tid);
-  }
-  __syncthreads();
+  const TileLoader<D> tl(wave, lane, static_cast<int>(p.np));
+  const OperandMap<D> om(m, hh);
+  char* const vring = smem;                // V stages, then K stages
+  char* const kring = smem + C::kKBase;    // K stage base for the loads
+  const char* const kread = smem;          // ... for operand reads (offsets carry kKBase)
 
-
-  // Step j has two barrier-separated phases.  Stage j&1 holds K_j and
-  // V_{j-1} during both; K_{j+1} and V_j go to stage (j+1)&1 (free since step
-  // j-1 ended): loaded into registers at the start of step j and stored at
-  // its end, two phases later.  MFMA phase of step j: S_j = K_j . Q^T and
-  // O += P_{j-1} . V_{j-1}; softmax phase: S_j -> P_j.  Role 0 runs (MFMA,
-  // softmax) of step j, role 1 runs (softmax of j-1, MFMA of j).  Each role
-  // has its own copy of the loop (same barrier sequence), so neither carries
-  // the other's register assignment.  Tiles a wave cannot see go through the
-  // masked softmax (P = 0), so the MFMA work is unconditional.
-  auto softmax_phase = [&](int j) __attribute__((always_inline)) {
-    if (j < w_main) {
-      softmax_tile<D, CAUSAL, false>(p, acc, ks, qs, j * kBN, qrow, hh, pf, o, m_run, l_run);
-    } else {
-      softmax_tile<D, CAUSAL, true>(p, acc, ks, qs, j * kBN, qrow, hh, pf, o, m_run, l_run);
+  auto rescale_o = [&]() __attribute__((always_inline)) {
+    if (need) {
+      // keeps the block a real branch: without it the multiplies of O are
+      // speculated onto every step
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int db = 0; db < C::kDB; ++db) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      }
     }
   };
-  auto mfma_phase = [&](int j, bool with_pv) __attribute__((always_inline)) {
-    load_ks(p, ksp, j * kBN, ks);
-    qk_tile<D>(smem + (j & 1) * C::kKStage, qf, m, hh, acc);
-    if (with_pv) pv_tile<D>(smem + C::kVBase + (j & 1) * C::kVStage, pf, m, hh, o);
-  };
-  // tiles [0, n_main) need no mask for any wave of the block; they run in a
-  // loop with only the unmasked softmax (one register assignment for O), the
-  // rest (tail / diagonal, at most a few) in a loop that picks per wave
-  const int n_main = min(CAUSAL ? min(q0, p.sk) / kBN : p.sk / kBN, ntiles);
-  auto run = [&](auto role_tag) __attribute__((always_inline)) {
-    constexpr int ROLE = decltype(role_tag)::value;
-    auto step = [&](int j, auto masked_tag) __attribute__((always_inline)) {
-      constexpr bool GENERIC = decltype(masked_tag)::value;
-      const bool ld_k = j + 1 < ntiles;
-      tc.load(p, kbase, vbase, j * kBN + kBN, ld_k, false, tid);
-      tc.load(p, kbase, vbase, j * kBN, false, true, tid);
-      const int js = ROLE == 0 ? j : j - 1;  // the tile this wave's softmax phase handles
-      auto smax = [&]() __attribute__((always_inline)) {
-        if constexpr (GENERIC) {
-          softmax_phase(js);
+
+  if (ntiles > 0) {
+    // ---- prologue: K_0, K_1 and a zero V_{-1} (read by step 0's P.V with
+    // P = 0), then K_2 and V_0 (what every step issues: K_{j+3}, V_{j+1})
+    tl.issue_k(kbase, kring + 0 * C::kKStage, 0, kv_end, wave);
+    tl.issue_k(kbase, kring + 1 * C::kKStage, kBN, kv_end, wave);
+    tl.issue_v(p, vbase, vring + 2 * C::kVStage, -kBN, kv_end, wave);
+    wait_loads_barrier<0>();
+    tl.issue_k(kbase, kring + 2 * C::kKStage, 2 * kBN, kv_end, wave);
+    tl.issue_v(p, vbase, vring + 0 * C::kVStage, 0, kv_end, wave);
+    load_ks(p, ksp, 0, ks);
+    qk_tile<D>(kread, om, qf, s);
+
+    // Step j (stage index st = j % 3): wait for K_{j+1} and V_{j-1} (issued at
+    // step j-2), apply the pending O rescale, issue K_{j+3} into stage j%3 and
+    // V_{j+1} into stage (j+1)%3 (their previous tiles were last read in step
+    // j-1, which every wave has left at the barrier), then P_{j-1}.V_{j-1},
+    // the softmax of S_j and S_{j+1}, interleaved; S and P are rewritten in
+    // place (see chunk_piece).
+    // ST (0..2) is the compile-time stage of the unrolled unmasked loop, so
+    // every LDS operand address is a lane offset plus an immediate; ST = -1
+    // (masked loop) takes the stage at run time.
+    auto step = [&](int j, int st_rt, auto mask_tag, auto st_tag) __attribute__((always_inline)) {
+      constexpr bool MASKED = decltype(mask_tag)::value;
+      constexpr int ST = decltype(st_tag)::value;
+      const int st = ST >= 0 ? ST : st_rt;
+      const int st1 = st == 2 ? 0 : st + 1;
+      const int st2 = st == 0 ? 2 : st - 1;
+      wait_loads_barrier<C::kStepLoads>();
+      rescale_o();
+      tl.issue_k(kbase, kring + st * C::kKStage, (j + 3) * kBN, kv_end, wave);
+      tl.issue_v(p, vbase, vring + st1 * C::kVStage, (j + 1) * kBN, kv_end, wave);
+      if constexpr (!MASKED) {
+        using SM = TileSoftmax<D, CAUSAL, false>;
+        SM sm(p, s, ks, qs, j * kBN, qrow, hh);
+        StepMfma<D> mf(vring + st2 * C::kVStage, kread + st1 * C::kKStage, om);
+        mf.template read<0>();
+        mf.template read<1>();
+        step_chunks<D, SM>(std::make_integer_sequence<int, StepMfma<D>::kN>{}, mf, sm, pf, o, qf, s, m_run, l_run,
+                           alpha, need, pf);
+      } else {
+        // tail / diagonal tiles (a few per block): the same work in plain
+        // order, P.V (reads P) -> softmax (reads S, writes P) -> QK (writes S)
+        pv_tile<D>(vring + st2 * C::kVStage, om, pf, o);
+        auto softmax = [&](auto smask_tag) __attribute__((always_inline)) {
+          using SM = TileSoftmax<D, CAUSAL, decltype(smask_tag)::value>;
+          SM sm(p, s, ks, qs, j * kBN, qrow, hh);
+          run_all_pieces(sm, std::make_integer_sequence<int, SM::kPieces>{}, m_run, l_run, alpha, need, pf);
+        };
+        // this wave's keys of tile j are all live: inside the key range and,
+        // causal, left of the wave's first row
+        if (j * kBN + kBN - 1 <= (CAUSAL ? min(wrow0, p.sk - 1) : p.sk - 1)) {
+          softmax(std::false_type{});
         } else {
-          softmax_tile<D, CAUSAL, false>(p, acc, ks, qs, js * kBN, qrow, hh, pf, o, m_run, l_run);
+          softmax(std::true_type{});
         }
-      };
-      if constexpr (ROLE == 0) {
-        mfma_phase(j, j > 0);
-      } else {
-        if (j > 0) smax();
+        qk_tile<D>(kread + st1 * C::kKStage, om, qf, s);
       }
-      __syncthreads();
-      if constexpr (ROLE == 0) {
-        smax();
-      } else {
-        mfma_phase(j, j > 0);
-      }
-      tc.store(smem, (j + 1) & 1, ld_k, true, tid);
-      __syncthreads();
+      // P_j and the row statistics are consumed a step later; pinning them
+      // here keeps their computation in this step (otherwise it sinks past
+      // the next barrier and the step loses its VALU half)
+      asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(l_run), "v"(alpha));
+      // k scales of the next tile: issued here, after the step's last LDS
+      // read, because a pending scalar load makes every later LDS wait a full
+      // lgkmcnt(0) (scalar loads return out of order)
+      load_ks(p, ksp, (j + 1) * kBN, ks);
     };
-    int j = 0;
-    for (; j < n_main; ++j) step(j, std::false_type{});
-    for (; j < ntiles; ++j) step(j, std::true_type{});
-    // last step: only P.V of the last tile (V_{ntiles-1} in stage ntiles&1)
-    const char* v_last = smem + C::kVBase + (ntiles & 1) * C::kVStage;
-    if constexpr (ROLE == 0) {
-      pv_tile<D>(v_last, pf, m, hh, o);
-    } else {
-      softmax_phase(ntiles - 1);
+    int j = 0, st = 0;
+    for (; j + 3 <= n_main; j += 3) {
+      step(j, 0, std::false_type{}, std::integral_constant<int, 0>{});
+      step(j + 1, 1, std::false_type{}, std::integral_constant<int, 1>{});
+      step(j + 2, 2, std::false_type{}, std::integral_constant<int, 2>{});
     }
-    __syncthreads();
-    if constexpr (ROLE == 1) pv_tile<D>(v_last, pf, m, hh, o);
-  };
-  if (ntiles > 0) {
-    if (role == 0) run(std::integral_constant<int, 0>{});
-    else run(std::integral_constant<int, 1>{});
+    for (; j < ntiles; ++j) {
+      step(j, st, std::true_type{}, std::integral_constant<int, -1>{});
+      st = st == 2 ? 0 : st + 1;
+    }
+    // last P.V: V_{ntiles-1} sits in stage (ntiles-1) % 3
+    wait_loads_barrier<C::kStepLoads>();
+    rescale_o();
+    pv_tile<D>(vring + (st == 0 ? 2 : st - 1) * C::kVStage, om, pf, o);
+    // loads of tiles past the end may still be in flight into this block's LDS
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
   // ---- epilogue: 1/l, cast, 8-byte stores (4 consecutive d per store)
