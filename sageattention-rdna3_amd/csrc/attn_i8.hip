@@ -141,25 +141,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 }
 
 // One 16-byte-per-lane buffer load straight into LDS (buffer_load_dwordx4
-// ... lds): the wave's 64 lanes fill 1 KB at `lds_dst` + lane*16; lanes whose
-// offset lies past the descriptor's end write zeros.  The builtin takes an
+// ... lds): the wave's 64 lanes fill 1 KB at `lds_dst` + lane*16 from byte
+// voffset + soffset of the buffer; lanes past the descriptor's end write
+// zeros.  The builtin takes an
 // LDS-address-space pointer, which only the device pass of this single-source
 // file can form; in the host pass (which compiles no device code but would
 // otherwise drop the kernels' launch stubs) the body is empty.
-__device__ __forceinline__ void lds_direct_load16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst, uint32_t voffset) {
+__device__ __forceinline__ void lds_direct_load16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst, uint32_t voffset,
+                                                  uint32_t soffset) {
 #if defined(__HIP_DEVICE_COMPILE__)
   typedef __attribute__((address_space(3))) void* lds_ptr;
   // the low 32 bits of a generic LDS address are the LDS offset
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, reinterpret_cast<lds_ptr>(reinterpret_cast<uintptr_t>(lds_dst)), 16,
-                                           voffset, 0, 0, 0);
+                                           voffset, soffset, 0, 0);
 #endif
 }
 
 // Tile loads straight from global memory into LDS.  Each wave instruction
-// fills 1 KB of LDS at M0 + lane*16, so a lane's source address picks the
+// fills 1 KB of LDS at M0 + lane*16, so a lane's source offset picks the
 // chunk that belongs at its LDS position (inverse swizzle; K rows also go
-// through kperm).  Descriptors end at the block's last key (kv_end), so tiles
-// past it, and K rows past it, read as zero without touching memory.
+// through kperm).  One descriptor per head and tensor, the tile's position in
+// the scalar offset: K ends at the block's last key (kv_end), so tiles and
+// rows past it read as zero without touching memory; V_T ends at its padded
+// row end (tiles past kv_end are loaded but never used).
 template <int D>
 struct TileLoader {
   using C = Cfg<D>;
@@ -184,20 +188,16 @@ struct TileLoader {
     }
   }
 
-  __device__ __forceinline__ void issue_k(const int8_t* kbase, char* kstage, int kt, int kv_end, int wave) const {
-    if (k_wave) {
-      const int rows = min(max(kv_end - kt, 0), kBN);
-      const auto rk = make_rsrc(kbase + static_cast<int64_t>(min(kt, kv_end)) * D, static_cast<uint32_t>(rows * D));
-      lds_direct_load16(rk, kstage + wave * 1024, k_goff);
-    }
+  // K rows kt.. through the head's K descriptor rk (rows past the block's
+  // last key read as zero) into the K stage at kstage.
+  __device__ __forceinline__ void issue_k(__amdgpu_buffer_rsrc_t rk, char* kstage, int kt, int wave) const {
+    if (k_wave) lds_direct_load16(rk, kstage + wave * 1024, k_goff, static_cast<uint32_t>(kt * D));
   }
-  __device__ __forceinline__ void issue_v(const AttnParams& p, const uint16_t* vbase, char* vstage, int kt, int kv_end,
-                                          int wave) const {
-    const bool live = kt >= 0 && kt < kv_end;
-    const int kc = live ? kt : 0;
-    const auto rv = make_rsrc(vbase + kc, live ? static_cast<uint32_t>((D * static_cast<int>(p.np) - kc) * 2) : 0u);
+  // V_T tokens kt.. through the head's V_T descriptor rv into the V stage at vstage.
+  __device__ __forceinline__ void issue_v(__amdgpu_buffer_rsrc_t rv, char* vstage, int kt, int wave) const {
 #pragma unroll
-    for (int i = 0; i < C::kVPerWave; ++i) lds_direct_load16(rv, vstage + (wave * C::kVPerWave + i) * 1024, v_goff[i]);
+    for (int i = 0; i < C::kVPerWave; ++i)
+      lds_direct_load16(rv, vstage + (wave * C::kVPerWave + i) * 1024, v_goff[i], static_cast<uint32_t>(kt * 2));
   }
 };
 
@@ -557,6 +557,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   float ks[4];
 
   const TileLoader<D> tl(wave, lane, static_cast<int>(p.np));
+  const auto rk = make_rsrc(kbase, static_cast<uint32_t>(kv_end * D));
+  const auto rv = make_rsrc(vbase, static_cast<uint32_t>(D * static_cast<int>(p.np) * 2));
   const OperandMap<D> om(m, hh);
   char* const vring = smem;                // V stages, then K stages
   char* const kring = smem + C::kKBase;    // K stage base for the loads
@@ -578,12 +580,12 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   if (ntiles > 0) {
     // ---- prologue: K_0, K_1 and a zero V_{-1} (read by step 0's P.V with
     // P = 0), then K_2 and V_0 (what every step issues: K_{j+3}, V_{j+1})
-    tl.issue_k(kbase, kring + 0 * C::kKStage, 0, kv_end, wave);
-    tl.issue_k(kbase, kring + 1 * C::kKStage, kBN, kv_end, wave);
-    tl.issue_v(p, vbase, vring + 2 * C::kVStage, -kBN, kv_end, wave);
+    tl.issue_k(rk, kring + 0 * C::kKStage, 0, wave);
+    tl.issue_k(rk, kring + 1 * C::kKStage, kBN, wave);
+    tl.issue_v(make_rsrc(vbase, 0u), vring + 2 * C::kVStage, 0, wave);
     wait_loads_barrier<0>();
-    tl.issue_k(kbase, kring + 2 * C::kKStage, 2 * kBN, kv_end, wave);
-    tl.issue_v(p, vbase, vring + 0 * C::kVStage, 0, kv_end, wave);
+    tl.issue_k(rk, kring + 2 * C::kKStage, 2 * kBN, wave);
+    tl.issue_v(rv, vring + 0 * C::kVStage, 0, wave);
     load_ks(p, ksp, 0, ks);
     qk_tile<D>(kread, om, qf, s);
 
@@ -604,8 +606,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
       const int st2 = st == 0 ? 2 : st - 1;
       wait_loads_barrier<C::kStepLoads>();
       rescale_o();
-      tl.issue_k(kbase, kring + st * C::kKStage, (j + 3) * kBN, kv_end, wave);
-      tl.issue_v(p, vbase, vring + st1 * C::kVStage, (j + 1) * kBN, kv_end, wave);
+      tl.issue_k(rk, kring + st * C::kKStage, (j + 3) * kBN, wave);
+      tl.issue_v(rv, vring + st1 * C::kVStage, (j + 1) * kBN, wave);
       if constexpr (!MASKED) {
         using SM = TileSoftmax<D, CAUSAL, false>;
         SM sm(p, s, ks, qs, j * kBN, qrow, hh);
@@ -724,7 +726,9 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
     return set_error(SAGE_ERR_ALIGNMENT, "sage_attn_i8_fwd: out needs an 8-byte aligned base and strides that are multiples of 4");
   const int64_t nqb = cdiv(q_len, kBM);
   const int64_t work = batch * q_heads * nqb;
-  if (q_len > INT32_MAX - kBM || kv_len > INT32_MAX - kBN || work > INT32_MAX)
+  const int64_t np = cdiv(kv_len, SAGE_VT_ALIGN) * SAGE_VT_ALIGN;
+  // per-head K and V_T are addressed through 32-bit buffer offsets
+  if (q_len > INT32_MAX - kBM || kv_len > INT32_MAX - kBN || work > INT32_MAX || head_dim * np * 2 > UINT32_MAX)
     return set_error(SAGE_ERR_UNSUPPORTED, "sage_attn_i8_fwd: sizes beyond 32-bit limits");
 
   AttnParams p;
@@ -737,7 +741,7 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
   p.o_sb = o_stride_b;
   p.o_sh = o_stride_h;
   p.o_sn = o_stride_n;
-  p.np = cdiv(kv_len, SAGE_VT_ALIGN) * SAGE_VT_ALIGN;
+  p.np = np;
   p.hq = static_cast<int32_t>(q_heads);
   p.hkv = static_cast<int32_t>(kv_heads);
   p.sq = static_cast<int32_t>(q_len);
