@@ -221,9 +221,31 @@ def main():
 
     n_k = max(args.steps, 10)
     ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5), n_k)
-    ms_quant = timed(lambda: ops.quant_qk_int8(q, k, mean, lay, D ** -0.5), n_k)
-    ms_vl = timed(lambda: ops.v_transpose(v, vt, lay), n_k)
-    ms_mean = timed(lambda: ops.mean_seq(k, lay), n_k) if smooth else 0.0
+    # The prologue kernels stream HBM: back to back on the same tensors, part of their traffic would hit the
+    # L2 / Infinity Cache (256 MB), so each launch gets its own input set out of NROT (together well past the
+    # caches), and the output of a set is written while the next set is read.
+    NROT = 3
+    qr = [q] + [q.clone() for _ in range(NROT - 1)]
+    kr = [k] + [k.clone() for _ in range(NROT - 1)]
+    vr = [v] + [v.clone() for _ in range(NROT - 1)]
+    vtr = [vt] + [torch.empty_like(vt) for _ in range(NROT - 1)]
+    rot = [0]
+
+    def rotated(fn):
+        def call():
+            i = rot[0] % NROT
+            rot[0] += 1
+            fn(i)
+        return call
+
+    # quant allocates its outputs per call (as the reference op does); holding each set's last outputs until
+    # the set comes round again keeps NROT + 1 output blocks in rotation instead of one reused block
+    qouts = [None] * NROT
+    ms_quant = timed(rotated(lambda i: qouts.__setitem__(i, ops.quant_qk_int8(qr[i], kr[i], mean, lay, D ** -0.5))),
+                     n_k)
+    ms_vl = timed(rotated(lambda i: ops.v_transpose(vr[i], vtr[i], lay)), n_k)
+    ms_mean = timed(rotated(lambda i: ops.mean_seq(kr[i], lay)), n_k) if smooth else 0.0
+    del qr, kr, vr, vtr, qouts
     torch.cuda.synchronize()
     achieved = ops_step / (ms_attn * 1e-3) / 1e12
     nq, nk = B * Hq * S * D, B * Hkv * S * D

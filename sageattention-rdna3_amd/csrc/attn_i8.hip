@@ -109,8 +109,6 @@ __device__ __forceinline__ int swz(int row) {
 // an involution).
 __device__ __forceinline__ int kperm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // max(x[lane], x[lane ^ 32]) / sum via v_permlane32_swap

@@ -99,7 +99,9 @@ __global__ __launch_bounds__(256) void quant_qk_i8_kernel(QuantParams p) {
   for (int i = 0; i < ITER; ++i) {
     const int row = row0 + i * RPI;
     if (row < S) {
-      raw[i] = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(row) * sn);
+      // streaming: each input byte is read once (non-temporal, no cache residency)
+      const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + static_cast<int64_t>(row) * sn));
+      raw[i] = make_uint4(t.x, t.y, t.z, t.w);
     } else {
       raw[i] = make_uint4(0, 0, 0, 0);
     }
@@ -176,7 +178,8 @@ __global__ __launch_bounds__(256) void quant_qk_i8_kernel(QuantParams p) {
       uint2 o;
       o.x = pack_i8x4(r8[0], r8[1], r8[2], r8[3]);
       o.y = pack_i8x4(r8[4], r8[5], r8[6], r8[7]);
-      *reinterpret_cast<uint2*>(dst + static_cast<int64_t>(row) * D) = o;
+      const u32x2_t ov = {o.x, o.y};
+      __builtin_nontemporal_store(ov, reinterpret_cast<u32x2_t*>(dst + static_cast<int64_t>(row) * D));
     }
   }
 }

@@ -31,6 +31,8 @@ typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef int int4_t __attribute__((ext_vector_type(4)));
 typedef int int16_t_ __attribute__((ext_vector_type(16)));
 typedef float float16_t_ __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // Two packed 16-bit values (one dword) -> two floats; exact for fp16 and bf16.
 template <bool BF16>
