@@ -117,6 +117,22 @@ int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t
                      int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                      int is_causal, void* stream);
 
+/*
+ * sage_attn_i8_fwd plus each row's log-sum-exp: lse [B,Hq,Sq] fp32
+ * contiguous (4-byte aligned; NULL = not written) receives
+ * ln(sum_j exp(s_ij)) over the natural-log scores s_ij = q_i.k_j * sm_scale
+ * after dequantisation (the log2-domain score times ln 2), -inf for a row with
+ * no live key.  The reference's return_lse returns a zero placeholder instead
+ * (sageattention/core.py:203-211); this is the value that placeholder stands
+ * for, usable to merge partial attentions over split key ranges.
+ */
+int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
+                         float* lse, const float* q_scale, const float* k_scale, int out_dtype,
+                         int64_t batch, int64_t q_heads, int64_t kv_heads,
+                         int64_t q_len, int64_t kv_len, int64_t head_dim,
+                         int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                         int is_causal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

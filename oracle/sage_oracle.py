@@ -25,6 +25,9 @@ What it restates (all citations are paths in LuXuxue/sageattention-rdna3):
                               exp2-domain softmax ``:656-689``, P rounded to
                               fp16 before PV ``csrc/mma_gfx11.h:97-106``, row sum
                               from unrounded p ``:689``, ``out*(1/l)`` ``:771``)
+* ``attn_i8_lse``          -- this build's real ``return_lse`` (the reference
+                              returns zeros, ``sageattention/core.py:203-211``):
+                              ln sum_j exp of the same scores, ln 2 * (m + log2 l)
 * ``sageattn``             -- ``sageattention/core.py:40-213`` (INT8 branch,
                               fp32 -> fp16 ``:78-83``, default ``sm_scale``
                               ``:65-66``, ``smooth_k`` default False ``:186``)
@@ -246,6 +249,25 @@ def v_layout(v, dtype, layout):
 # --------------------------------------------------------------------------
 # fused attention
 # --------------------------------------------------------------------------
+def _scores_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal):
+    """log2-domain scores s_ij = fl32(fl32(acc_ij) * fl32(qs[i//32] * ks[j//16])) as float64, masked
+    entries (j > i when causal, top-left) at -inf; GQA head map hkv = hq // (Hq/Hkv)
+    (csrc/attn_gfx11.cu:464,618-631)."""
+    Hq = q8.shape[1]
+    Hkv = k8.shape[1]
+    Sk = k8.shape[2]
+    hk = hq // (Hq // Hkv)
+    kf = k8[b, hk].astype(np.float32)
+    ks_col = k_scale[b, hk][np.arange(Sk) // K_GROUP].astype(np.float32)
+    acc = q8[b, hq, rows].astype(np.float32) @ kf.T
+    sc = (q_scale[b, hq][rows // Q_GROUP][:, None] * ks_col[None, :]).astype(np.float32)
+    s = (acc * sc).astype(np.float32).astype(np.float64)
+    if is_causal:
+        cols = np.arange(Sk)
+        s = np.where(cols[None, :] <= rows[:, None], s, -np.inf)
+    return s, hk
+
+
 def attn_i8_rows(q8, k8, v_t, q_scale, k_scale, b, hq, rows, is_causal, n_kv_heads=None):
     """Attention output (float64, before the output cast) for selected rows of one head.
 
@@ -255,23 +277,13 @@ def attn_i8_rows(q8, k8, v_t, q_scale, k_scale, b, hq, rows, is_causal, n_kv_hea
         p_ij = exp2(s_ij - max_j s_ij), l_i = sum_j p_ij (unrounded)
         o_i  = sum_j fp16(p_ij) * V_ij / l_i   (l_i == 0 -> 0)
     """
-    Hq = q8.shape[1]
-    Hkv = k8.shape[1]
     Sk = k8.shape[2]
-    hk = hq // (Hq // Hkv)
     rows = np.asarray(rows, dtype=np.int64)
     D = q8.shape[3]
     if Sk == 0 or rows.size == 0:
         return np.zeros((rows.size, D), np.float64)
-    kf = k8[b, hk].astype(np.float32)
+    s, hk = _scores_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal)
     vf = v_t[b, hk, :, :Sk].astype(np.float64).T
-    ks_col = k_scale[b, hk][np.arange(Sk) // K_GROUP].astype(np.float32)
-    acc = q8[b, hq, rows].astype(np.float32) @ kf.T
-    sc = (q_scale[b, hq][rows // Q_GROUP][:, None] * ks_col[None, :]).astype(np.float32)
-    s = (acc * sc).astype(np.float32).astype(np.float64)
-    if is_causal:
-        cols = np.arange(Sk)
-        s = np.where(cols[None, :] <= rows[:, None], s, -np.inf)
     m = s.max(axis=1, keepdims=True)
     m = np.where(np.isfinite(m), m, 0.0)
     p = np.exp2(s - m)
@@ -281,6 +293,37 @@ def attn_i8_rows(q8, k8, v_t, q_scale, k_scale, b, hq, rows, is_causal, n_kv_hea
     with np.errstate(invalid="ignore", divide="ignore"):
         o = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
     return o
+
+
+def attn_i8_lse_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal):
+    """Log-sum-exp (float64) of selected rows: ln sum_j exp(s_ij * ln 2) over the natural-log scores
+    (s_ij as in ``attn_i8_rows``, masked keys excluded), -inf for a row without a live key.
+
+    Not in the reference: its ``return_lse`` returns zeros (sageattention/core.py:203-211).  This is
+    the quantity that placeholder stands for, restated from the same scores the output uses.
+    """
+    Sk = k8.shape[2]
+    rows = np.asarray(rows, dtype=np.int64)
+    if Sk == 0 or rows.size == 0:
+        return np.full(rows.size, -np.inf)
+    s, _ = _scores_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal)
+    m = s.max(axis=1)
+    mf = np.where(np.isfinite(m), m, 0.0)
+    l = np.exp2(s - mf[:, None]).sum(axis=1)
+    with np.errstate(divide="ignore"):
+        return np.where(l > 0, (mf + np.log2(np.where(l > 0, l, 1.0))) * np.log(2.0), -np.inf)
+
+
+def attn_i8_lse(q8, k8, q_scale, k_scale, is_causal, row_block=512):
+    """``attn_i8_lse_rows`` over every row: [B,Hq,Sq] float64."""
+    B, Hq, Sq, _ = q8.shape
+    out = np.zeros((B, Hq, Sq), np.float64)
+    for b in range(B):
+        for h in range(Hq):
+            for r0 in range(0, Sq, row_block):
+                rows = np.arange(r0, min(Sq, r0 + row_block))
+                out[b, h, rows] = attn_i8_lse_rows(q8, k8, q_scale, k_scale, b, h, rows, is_causal)
+    return out
 
 
 def attn_i8(q8, k8, v_t, q_scale, k_scale, is_causal, out_dtype, row_block=512):

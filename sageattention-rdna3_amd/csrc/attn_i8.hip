@@ -57,6 +57,7 @@ struct AttnParams {
   const int8_t* k8;      // [B,Hkv,Sk,D]
   const uint16_t* vt;    // fp16 [B,Hkv,D,np]
   void* out;
+  float* lse;            // [B,Hq,Sq] or null
   const float* q_scale;  // [B,Hq,ceil(Sq/32)]
   const float* k_scale;  // [B,Hkv,ceil(Sk/16)]
   int64_t o_sb, o_sh, o_sn;
@@ -659,8 +660,14 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  // ---- epilogue: 1/l, cast, 8-byte stores (4 consecutive d per store)
+  // ---- epilogue: 1/l, cast, 8-byte stores (4 consecutive d per store); LSE =
+  // ln(sum_j e^{s_j}) over the natural-log scores s_j = ln2 * (log2-domain
+  // score) = ln2 * (m + log2 l), -inf for a row without a live key
   const float l_tot = xhalf_sum(l_run);
+  if (p.lse != nullptr && qrow < p.sq && hh == 0) {
+    p.lse[static_cast<int64_t>(bh) * p.sq + qrow] =
+        (l_tot > 0.0f) ? (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f : -INFINITY;
+  }
   if (qrow < p.sq) {
     const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
     uint16_t* op = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(b) * p.o_sb +
@@ -699,41 +706,43 @@ void launch(const AttnParams& p, bool out_bf16, hipStream_t st) {
 
 using namespace sage;
 
-extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
-                                const float* q_scale, const float* k_scale, int out_dtype,
-                                int64_t batch, int64_t q_heads, int64_t kv_heads,
-                                int64_t q_len, int64_t kv_len, int64_t head_dim,
-                                int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
-                                int is_causal, void* stream) {
-  clear_error();
+namespace {
+
+int attn_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out, float* lse, const float* q_scale,
+             const float* k_scale, int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t q_len,
+             int64_t kv_len, int64_t head_dim, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+             int is_causal, void* stream, const char* fn) {
   if (out_dtype != SAGE_DTYPE_F16 && out_dtype != SAGE_DTYPE_BF16)
     return set_error(SAGE_ERR_INVALID_ARG, "out_dtype must be SAGE_DTYPE_F16 or SAGE_DTYPE_BF16, got %d", out_dtype);
   if (head_dim != 64 && head_dim != 128)
     return set_error(SAGE_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld", static_cast<long long>(head_dim));
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || q_len < 0 || kv_len < 0)
-    return set_error(SAGE_ERR_INVALID_ARG, "sage_attn_i8_fwd: negative or zero size");
+    return set_error(SAGE_ERR_INVALID_ARG, "%s: negative or zero size", fn);
   if (q_heads % kv_heads != 0)
     return set_error(SAGE_ERR_INVALID_ARG, "q_heads (%lld) must be a multiple of kv_heads (%lld)",
                      static_cast<long long>(q_heads), static_cast<long long>(kv_heads));
   if (batch == 0 || q_len == 0) return SAGE_OK;
   if (!out || !q_i8 || !q_scale || (kv_len > 0 && (!k_i8 || !k_scale || !value_t)))
-    return set_error(SAGE_ERR_INVALID_ARG, "sage_attn_i8_fwd: null pointer argument");
+    return set_error(SAGE_ERR_INVALID_ARG, "%s: null pointer argument", fn);
   if (!aligned(q_i8, 16) || (kv_len > 0 && (!aligned(k_i8, 16) || !aligned(value_t, 16))))
-    return set_error(SAGE_ERR_ALIGNMENT, "sage_attn_i8_fwd: q_i8/k_i8/value_t must be 16-byte aligned");
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: q_i8/k_i8/value_t must be 16-byte aligned", fn);
   if (!aligned(out, 8) || (o_stride_b % 4) || (o_stride_h % 4) || (o_stride_n % 4))
-    return set_error(SAGE_ERR_ALIGNMENT, "sage_attn_i8_fwd: out needs an 8-byte aligned base and strides that are multiples of 4");
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: out needs an 8-byte aligned base and strides that are multiples of 4", fn);
+  if (lse != nullptr && !aligned(lse, 4))
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: lse must be 4-byte aligned", fn);
   const int64_t nqb = cdiv(q_len, kBM);
   const int64_t work = batch * q_heads * nqb;
   const int64_t np = cdiv(kv_len, SAGE_VT_ALIGN) * SAGE_VT_ALIGN;
   // per-head K and V_T are addressed through 32-bit buffer offsets
   if (q_len > INT32_MAX - kBM || kv_len > INT32_MAX - kBN || work > INT32_MAX || head_dim * np * 2 > UINT32_MAX)
-    return set_error(SAGE_ERR_UNSUPPORTED, "sage_attn_i8_fwd: sizes beyond 32-bit limits");
+    return set_error(SAGE_ERR_UNSUPPORTED, "%s: sizes beyond 32-bit limits", fn);
 
   AttnParams p;
   p.q8 = q_i8;
   p.k8 = k_i8;
   p.vt = static_cast<const uint16_t*>(value_t);
   p.out = out;
+  p.lse = lse;
   p.q_scale = q_scale;
   p.k_scale = k_scale;
   p.o_sb = o_stride_b;
@@ -758,5 +767,29 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
     if (is_causal) launch<64, true>(p, bf16, st);
     else launch<64, false>(p, bf16, st);
   }
-  return check_launch("sage_attn_i8_fwd");
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
+                                const float* q_scale, const float* k_scale, int out_dtype,
+                                int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                int is_causal, void* stream) {
+  clear_error();
+  return attn_fwd(q_i8, k_i8, value_t, out, nullptr, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads, q_len,
+                  kv_len, head_dim, o_stride_b, o_stride_h, o_stride_n, is_causal, stream, "sage_attn_i8_fwd");
+}
+
+extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
+                                    float* lse, const float* q_scale, const float* k_scale, int out_dtype,
+                                    int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                    int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                    int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                    int is_causal, void* stream) {
+  clear_error();
+  return attn_fwd(q_i8, k_i8, value_t, out, lse, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads, q_len,
+                  kv_len, head_dim, o_stride_b, o_stride_h, o_stride_n, is_causal, stream, "sage_attn_i8_fwd_lse");
 }

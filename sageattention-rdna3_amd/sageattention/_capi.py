@@ -52,6 +52,9 @@ SIGNATURES = {
     "sage_attn_i8_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I,
                               _I64, _I64, _I64, _I64, _I64, _I64,
                               _I64, _I64, _I64, _I, _P]),
+    "sage_attn_i8_fwd_lse": (_I, [_P, _P, _P, _P, _P, _P, _P, _I,
+                                  _I64, _I64, _I64, _I64, _I64, _I64,
+                                  _I64, _I64, _I64, _I, _P]),
 }
 
 

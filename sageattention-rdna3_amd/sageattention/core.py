@@ -1,8 +1,9 @@
 """Drop-in ``sageattn`` for MI355X: the INT8 quantized path on gfx950 kernels.
 
 Mirrors ``sageattention/core.py:40-233`` of the reference (same signature,
-defaults, assertion messages, fp32 handling, ``smooth_k`` default False,
-``return_lse`` placeholder and the upstream alias).  Every call takes the
+defaults, assertion messages, fp32 handling, ``smooth_k`` default False and
+the upstream alias); ``return_lse`` returns the real log-sum-exp where the
+reference returns a zero placeholder.  Every call takes the
 INT8 path; the reference's Triton backend, ``SAGEATTN_BACKEND`` switch and the
 direct fp16/bf16 branch (core.py:8,68-76,113-164) do not exist here.
 """
@@ -37,8 +38,10 @@ def sageattn(
     ``smooth_k=True``), fp16 V, fused INT8-QK^T / fp16-PV flash attention.
 
     q: [B,Hq,Sq,D] (HND) or [B,Sq,Hq,D] (NHD); k, v with Hkv heads (Hq % Hkv == 0).
-    Returns o with q's shape, layout and dtype (and a zero LSE placeholder
-    [B,Hq,Sq] fp32 when ``return_lse``).  Unknown kwargs are ignored.
+    Returns o with q's shape, layout and dtype (and, when ``return_lse``, the
+    rows' log-sum-exp [B,Hq,Sq] fp32: ln sum_j exp(sm_scale * q_i.k_j) after
+    quantisation, -inf for a row with no key; the reference returns zeros).
+    Unknown kwargs are ignored.
     """
     dtype = q.dtype
     assert q.is_cuda, "Input tensors must be on CUDA/HIP device."
@@ -99,15 +102,16 @@ def sageattn(
     else:
         k_mean = torch.empty(0, device=q.device, dtype=q.dtype)
     q_int8, q_scale, k_int8, k_scale = ops.quant_qk_int8(q, k, k_mean, layout_code, sm_scale)
+    # return_lse: the reference returns a zero placeholder (core.py:203-211); the fused kernel writes
+    # the real log-sum-exp of each row (natural log, scaled scores; -inf for a row without keys)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
     ops.qk_int8_sv_bf16_attn_t(q_int8, k_int8, v_t, o, q_scale, k_scale,
-                               layout_code, int(is_causal), sm_scale)
+                               layout_code, int(is_causal), sm_scale, lse=lse)
 
     if input_dtype == torch.float32:
         o = o.to(torch.float32)
 
     if return_lse:
-        # the reference returns a zero placeholder (core.py:203-211)
-        lse = torch.zeros((B, Hq, Sq), dtype=torch.float32, device=q.device)
         return o, lse
 
     return o

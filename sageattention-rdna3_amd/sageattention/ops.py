@@ -9,7 +9,7 @@ stream.  ``tensor_layout`` is the reference's integer code: 1 = HND
 from __future__ import annotations
 
 import ctypes
-from typing import List
+from typing import List, Optional
 
 import torch
 
@@ -105,10 +105,13 @@ def v_transpose(value: torch.Tensor, value_t: torch.Tensor, tensor_layout: int) 
 
 def qk_int8_sv_bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                            output: torch.Tensor, q_scale: torch.Tensor, k_scale: torch.Tensor,
-                           tensor_layout: int, is_causal: int, sm_scale: float) -> torch.Tensor:
+                           tensor_layout: int, is_causal: int, sm_scale: float,
+                           lse: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused attention over quantised Q/K and V_T into ``output`` (reference
     qk_int8_sv_bf16_attn_t, csrc/attn_gfx11.cu:2069-2273).  ``sm_scale`` is
-    unused: it is already folded into ``q_scale`` (as in the reference)."""
+    unused: it is already folded into ``q_scale`` (as in the reference).
+    ``lse`` (this build's addition; contiguous fp32 [B,Hq,Sq]) receives each
+    row's natural-log log-sum-exp of the scaled scores."""
     B, Hq, Sq, D = query.shape
     Bk, Hkv, Sk, Dk = key.shape
     if Bk != B or Dk != D:
@@ -126,6 +129,14 @@ def qk_int8_sv_bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.
     (Bo, Ho, So, Do), (osb, osh, osn) = _bhnd(output, tensor_layout)
     if (Bo, Ho, So, Do) != (B, Hq, Sq, D) or output.stride(-1) != 1:
         raise ValueError("output shape does not match the query")
+    if lse is not None:
+        if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+            raise ValueError(f"lse must be contiguous fp32 [{B},{Hq},{Sq}]")
+        with torch.cuda.device(query.device):
+            _capi.call("sage_attn_i8_fwd_lse", _ptr(query), _ptr(key), _ptr(value), _ptr(output), _ptr(lse),
+                       _ptr(q_scale), _ptr(k_scale), _dtype_code(output),
+                       B, Hq, Hkv, Sq, Sk, D, osb, osh, osn, int(bool(is_causal)), _stream(query))
+        return output
     with torch.cuda.device(query.device):
         _capi.call("sage_attn_i8_fwd", _ptr(query), _ptr(key), _ptr(value), _ptr(output),
                    _ptr(q_scale), _ptr(k_scale), _dtype_code(output),

@@ -117,6 +117,32 @@ def test_attn_zero_work_is_ok(lib):
     assert attn(lib, B=0) == _capi.OK
 
 
+def attn_lse(lib, **kw):
+    a = dict(q8=FAKE, k8=FAKE, vt=FAKE, o=FAKE, lse=FAKE, qs=FAKE, ks=FAKE, dtype=0, B=1, Hq=4, Hkv=2, Sq=64,
+             Sk=64, D=128, osb=4 * 64 * 128, osh=64 * 128, osn=128, causal=0, stream=NULL)
+    a.update(kw)
+    return lib.sage_attn_i8_fwd_lse(*a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        (dict(dtype=2), _capi.ERR_INVALID_ARG, "out_dtype"),
+        (dict(vt=NULL), _capi.ERR_INVALID_ARG, "sage_attn_i8_fwd_lse: null"),
+        (dict(lse=ODD), _capi.ERR_ALIGNMENT, "lse must be 4-byte aligned"),
+        (dict(Sq=2 ** 31), _capi.ERR_UNSUPPORTED, "32-bit"),
+    ],
+)
+def test_attn_lse_validation(lib, kw, code, msg):
+    assert attn_lse(lib, **kw) == code
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_attn_lse_zero_work_is_ok(lib):
+    assert attn_lse(lib, Sq=0) == _capi.OK
+    assert attn_lse(lib, B=0, lse=NULL) == _capi.OK
+
+
 def test_v_layout_and_mean_validation(lib):
     assert lib.sage_v_layout(FAKE, FAKE, 0, 1, 2, 100, 80, 0, 0, 0, NULL) == _capi.ERR_UNSUPPORTED
     assert lib.sage_v_layout(ODD, FAKE, 0, 1, 2, 100, 64, 0, 6400, 64, NULL) == _capi.ERR_ALIGNMENT

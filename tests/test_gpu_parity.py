@@ -177,3 +177,71 @@ def test_nondefault_stream_and_repeat_are_identical():
     s.synchronize()
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+# ------------------------------------------------------------------ LSE (this build's real return_lse)
+def gpu_attn_lse(cfg: Config, pro, dtype, q8=None, k8=None, vt=None, qs=None, ks=None):
+    from sageattention import ops
+
+    lay = ops.HND if cfg.layout == "HND" else ops.NHD
+    q8 = pro["q8"] if q8 is None else q8
+    k8 = pro["k8"] if k8 is None else k8
+    vt = pro["v_t"] if vt is None else vt
+    qs = pro["q_scale"] if qs is None else qs
+    ks = pro["k_scale"] if ks is None else ks
+    B, Hq, Sq, D = q8.shape
+    shape = (B, Hq, Sq, D) if cfg.layout == "HND" else (B, Sq, Hq, D)
+    o = torch.empty(shape, device="cuda", dtype=dtype)
+    lse = torch.empty((B, Hq, Sq), device="cuda", dtype=torch.float32)
+    ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(cfg.causal), D ** -0.5, lse=lse)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+@pytest.mark.parametrize("cfg", [SMALL[1], SMALL[2], SMALL[3], SMALL[4], SMALL[8], SMALL[9]], ids=lambda c: c.name)
+def test_lse_vs_oracle(cfg):
+    """Each row's log-sum-exp against the oracle's (same INT8 inputs):
+    |gpu - oracle| <= 2e-4 + 2e-6 |oracle| (fp32 sums of hardware exp2 and the FMA-folded dequant);
+    rows without a live key are -inf on both sides.  The output is unchanged by asking for the LSE."""
+    _say(f"[lse] {cfg}")
+    q, k, v = make_inputs(cfg, seed=3)
+    pro = gpu_prologue(cfg, q, k, v)
+    o, lse = gpu_attn_lse(cfg, pro, q.dtype)
+    o_plain = gpu_attn(cfg, pro, q.dtype)
+    assert torch.equal(o, o_plain)
+    q8, qs, k8, ks = (to_np(pro[n]) for n in ("q8", "q_scale", "k8", "k_scale"))
+    ref = orc.attn_i8_lse(q8, k8, qs, ks, cfg.causal)
+    got = to_np(lse).astype(np.float64)
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    err = np.abs(got[fin] - ref[fin])
+    assert np.all(err <= 2e-4 + 2e-6 * np.abs(ref[fin])), f"worst {err.max():.3g}"
+    _say(f"  worst |lse gpu - oracle| = {err.max():.3g}")
+
+
+def test_lse_merges_split_kv():
+    """Size-independent property: attention over keys [0, S/2) and [S/2, S) separately, merged with
+    their LSEs (lse = logaddexp(lse1, lse2), o = sum_i o_i exp(lse_i - lse)), equals attention over
+    all keys (same quantised inputs; fp16 outputs, so the merge adds about one output ulp)."""
+    cfg = Config("split", 1, 4, 2, 4096, 128, "fp16", "HND", False, False)
+    _say(f"[lse split] {cfg}")
+    q, k, v = make_inputs(cfg, seed=4)
+    pro = gpu_prologue(cfg, q, k, v)
+    o_full, lse_full = gpu_attn_lse(cfg, pro, torch.float16)
+    half = cfg.S // 2
+    parts = []
+    for a, b in ((0, half), (half, cfg.S)):
+        k8 = pro["k8"][:, :, a:b].contiguous()
+        ks = pro["k_scale"][:, :, a // 16:b // 16].contiguous()
+        vt = pro["v_t"][:, :, :, a:b].contiguous()
+        parts.append(gpu_attn_lse(cfg, pro, torch.float16, k8=k8, vt=vt, ks=ks))
+    (o1, l1), (o2, l2) = parts
+    lse_m = torch.logaddexp(l1, l2)
+    w1, w2 = torch.exp(l1 - lse_m)[..., None], torch.exp(l2 - lse_m)[..., None]
+    o_m = o1.float() * w1 + o2.float() * w2
+    assert torch.max(torch.abs(lse_m - lse_full)).item() < 1e-4
+    err = torch.max(torch.abs(o_m - o_full.float())).item()
+    cs = cos_sim(to_np(o_m), to_np(o_full.float()))
+    _say(f"  merged vs full: max |lse| diff {torch.max(torch.abs(lse_m - lse_full)).item():.3g}, "
+         f"max |o| diff {err:.3g}, cos {cs:.7f}")
+    assert err < 3e-3 and cs > 0.99999

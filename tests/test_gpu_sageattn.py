@@ -176,13 +176,20 @@ class TestApiContract:
         assert out.dtype == torch.float32
         assert_close(out, reference_attention(q, k, v), torch.float16, oracle_attention(q, k, v, "HND", False))
 
-    def test_return_lse_placeholder(self, sageattn):
+    def test_return_lse(self, sageattn):
+        # the reference returns a zero placeholder (core.py:203-211); this build returns the real
+        # log-sum-exp of each row, checked against the oracle's on the same quantised inputs
         q, k, v = (randn(2, 3, 100, 128) for _ in range(3))
-        o, lse = sageattn(q, k, v, return_lse=True)
-        assert lse.shape == (2, 3, 100) and lse.dtype == torch.float32 and torch.all(lse == 0)
+        o, lse = sageattn(q, k, v, return_lse=True, is_causal=True)
+        assert lse.shape == (2, 3, 100) and lse.dtype == torch.float32
+        assert torch.equal(o, sageattn(q, k, v, is_causal=True))
+        _, inter = orc.sageattn(*(to_np(t) for t in (q, k, v)), "fp16", "HND", True, intermediates=True)
+        ref = orc.attn_i8_lse(inter["q8"], inter["k8"], inter["q_scale"], inter["k_scale"], True)
+        assert np.max(np.abs(to_np(lse).astype(np.float64) - ref)) < 2e-4
         qn = q.transpose(1, 2).contiguous()
-        o, lse = sageattn(qn, k.transpose(1, 2), v.transpose(1, 2), tensor_layout="NHD", return_lse=True)
-        assert lse.shape == (2, 3, 100)
+        o2, lse2 = sageattn(qn, k.transpose(1, 2), v.transpose(1, 2), tensor_layout="NHD", return_lse=True,
+                            is_causal=True)
+        assert lse2.shape == (2, 3, 100) and torch.equal(lse2, lse)
 
     def test_alias_and_unknown_kwargs(self, sageattn):
         from sageattention import sageattn_qk_int8_pv_fp16_cuda

@@ -313,6 +313,44 @@ def test_attention_constant_v_normalises():
     assert np.all(np.abs(o - 0.5) < 2e-3)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_lse_matches_scipy_logsumexp_of_fp64_dequant_scores(causal):
+    """The oracle's LSE (this build's real return_lse) against scipy's logsumexp over independently
+    dequantised fp64 scores in natural-log units (the log2-domain scores times ln 2)."""
+    from scipy.special import logsumexp
+
+    rng = np.random.default_rng(17)
+    B, Hq, Hkv, S, D = 1, 4, 2, 130, 64
+    q = rng.standard_normal((B, Hq, S, D)).astype(np.float16)
+    k = rng.standard_normal((B, Hkv, S, D)).astype(np.float16)
+    q8, qs, k8, ks = orc.quant_qk_int8(q, k, "fp16", "HND", D ** -0.5)
+    lse = orc.attn_i8_lse(q8, k8, qs, ks, causal)
+    qd = q8.astype(np.float64) * np.repeat(qs, 32, axis=-1)[..., :S, None]
+    kd = np.repeat(k8.astype(np.float64) * np.repeat(ks, 16, axis=-1)[..., :S, None], Hq // Hkv, axis=1)
+    sn = (qd @ kd.transpose(0, 1, 3, 2)) * math.log(2.0)
+    if causal:
+        sn = np.where(np.arange(S)[None, :] <= np.arange(S)[:, None], sn, -np.inf)
+    ref = logsumexp(sn, axis=-1)
+    # only the fp32 rounding of qs*ks and of acc*(qs*ks) separates the two
+    assert np.max(np.abs(lse - ref) / np.maximum(1.0, np.abs(ref))) < 1e-6
+
+
+def test_lse_closed_forms():
+    # all-zero Q: every live score is 0, so lse = ln(#live keys): ln(Sk), causal row i -> ln(i + 1)
+    q8 = np.zeros((1, 1, 40, 64), np.int8)
+    k8 = np.random.default_rng(18).integers(-127, 128, (1, 1, 40, 64)).astype(np.int8)
+    qs, ks = np.full((1, 1, 2), 0.01, np.float32), np.full((1, 1, 3), 0.02, np.float32)
+    assert np.allclose(orc.attn_i8_lse(q8, k8, qs, ks, False), math.log(40), rtol=0, atol=1e-12)
+    assert np.allclose(orc.attn_i8_lse(q8, k8, qs, ks, True)[0, 0], np.log(np.arange(1, 41)), rtol=0, atol=1e-12)
+    # one key: lse = s * ln 2 exactly as the score; no key: -inf
+    q8 = np.full((1, 1, 1, 64), 3, np.int8)
+    k8 = np.full((1, 1, 1, 64), -2, np.int8)
+    s = np.float32(np.float32(3 * -2 * 64) * np.float32(np.float32(0.01) * np.float32(0.02)))
+    assert orc.attn_i8_lse(q8, k8, qs[..., :1], ks[..., :1], False)[0, 0, 0] == float(s) * math.log(2.0)
+    empty = orc.attn_i8_lse(q8, np.zeros((1, 1, 0, 64), np.int8), qs[..., :1], np.zeros((1, 1, 0), np.float32), False)
+    assert np.all(np.isneginf(empty))
+
+
 def test_attention_empty_kv_gives_zero():
     q8 = np.ones((1, 1, 5, 64), np.int8)
     k8 = np.zeros((1, 1, 0, 64), np.int8)
