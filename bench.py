@@ -143,6 +143,70 @@ def kernels_only(cfg, q, k, v, n):
     log(f"[bench] kernels-only: {n} x path kernels + {n} x 1 GiB copy done")
 
 
+# direct (unquantised) kernel: the largest D=128 self-attention shape the reference's dispatch sends to it
+DIRECT_CFG = (1, 32, 32, 2048, 128, "bf16", "HND", True, False)
+
+
+def direct_probe(dev, n):
+    """The direct fp16/bf16 kernel alone (HIP events on its launch stream) at DIRECT_CFG, against the
+    dense bf16 MFMA peak, and a whole ``sageattn`` call at that shape through either path (the
+    direct path, and the INT8 path with the direct thresholds switched off)."""
+    import torch
+
+    from sageattention import ops, sageattn
+
+    B, Hq, Hkv, S, D, dt, layout, causal, smooth = DIRECT_CFG
+    q, k, v = make_inputs(DIRECT_CFG, dev)
+    lay = ops.HND if layout == "HND" else ops.NHD
+    vt = torch.empty(B, Hkv, D, (S + 63) // 64 * 64, device=dev, dtype=torch.float16)
+    ops.v_transpose(v, vt, lay)
+    o = torch.empty_like(q)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        for _ in range(3):
+            fn()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    ms_kernel = timed(lambda: ops.bf16_attn_t(q, k, vt, o, lay, int(causal), D ** -0.5, 0))
+    ms_direct = timed(lambda: sageattn(q, k, v, tensor_layout=layout, is_causal=causal))
+    names = ["SAGEATTN_DIRECT_THRESHOLD_D128", "SAGEATTN_DIRECT_THRESHOLD_D128_CROSS"]
+    saved = {x: os.environ.get(x) for x in names}
+    try:
+        for x in names:
+            os.environ[x] = "-1"
+        ms_int8 = timed(lambda: sageattn(q, k, v, tensor_layout=layout, is_causal=causal))
+    finally:
+        for x, val in saved.items():
+            if val is None:
+                os.environ.pop(x, None)
+            else:
+                os.environ[x] = val
+    flops = attn_ops(B, Hq, S, S, D, causal)
+    achieved = flops / (ms_kernel * 1e-3) / 1e12
+    log(f"[bench] direct kernel {ms_kernel:.4f} ms = {achieved:.1f} TFLOP/s "
+        f"({100 * achieved / PEAK_F16_TFLOPS:.1f}% bf16 peak); sageattn at this shape: direct {ms_direct:.4f} ms, "
+        f"int8 path {ms_int8:.4f} ms")
+    return {
+        "workload": f"bf16_attn_t B{B} Hq{Hq} S{S} D{D} {dt} {layout} {'causal' if causal else 'non-causal'}",
+        "kernel": "attn_fwd_kernel (bf16 QK)",
+        "kernel_ms": round(ms_kernel, 5),
+        "achieved": round(achieved, 2),
+        "peak": PEAK_F16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_F16_TFLOPS, 4),
+        "sageattn_direct_ms": round(ms_direct, 5),
+        "sageattn_int8_ms": round(ms_int8, 5),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,6 +321,8 @@ def main():
         f"quant {ms_quant * 1e3:.1f} us = {quant_bytes / ms_quant / 1e6:.0f} GB/s; "
         f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s")
 
+    direct = direct_probe(dev, n_k)
+
     traffic = None
     tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")
     if os.path.exists(tfile):
@@ -296,7 +362,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_INT8_TOPS, 4),
             "traffic": traffic,
-            "kernel": "attn_i8_fwd_kernel",
+            "kernel": "attn_fwd_kernel (int8 QK)",
             "kernel_ms": round(ms_attn, 5),
             "frac_of_mixed_int8_fp16_ceiling": round(achieved / mixed, 4),
         },
@@ -309,6 +375,7 @@ def main():
             "k_mean_us": round(ms_mean * 1e3, 2) if smooth else None,
             "k_mean_GBps": round(mean_bytes / ms_mean / 1e6, 1) if smooth else None,
         },
+        "direct": direct,
         "device": {"name": props.name, "cus": props.multi_processor_count},
         "cpu_baseline": cpu,
     }

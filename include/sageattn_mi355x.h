@@ -15,8 +15,9 @@
  *
  * Reference interfaces replaced (LuXuxue/sageattention-rdna3):
  *   torch.ops.sageattention.{mean_seq, quant_qk_int8, v_transpose,
- *   qk_int8_sv_bf16_attn_t}, declared at csrc/pybind_gfx11.cpp:18-38 and
- *   csrc/attn_gfx11.h:10-51, implemented at csrc/attn_gfx11.cu:1889-2273.
+ *   qk_int8_sv_bf16_attn_t, fp16_attn_t, bf16_attn_t}, declared at
+ *   csrc/pybind_gfx11.cpp:18-38 and csrc/attn_gfx11.h:10-51, implemented at
+ *   csrc/attn_gfx11.cu:1889-2472.
  */
 #ifndef SAGEATTN_MI355X_H
 #define SAGEATTN_MI355X_H
@@ -132,6 +133,27 @@ int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* val
                          int64_t q_len, int64_t kv_len, int64_t head_dim,
                          int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                          int is_causal, void* stream);
+
+/*
+ * Direct attention without quantisation (the reference's short-sequence
+ * branch): S = fp32(q . k) * fl(fl(sm_scale) * log2 e) from fp16/bf16 Q and K
+ * (fp32 accumulation), the same masks and online softmax as sage_attn_i8_fwd,
+ * P rounded to fp16, O = P . V_T with V_T from sage_v_layout, out = O / rowsum
+ * cast to `dtype` (the type of query, key and out).  query/key are read in
+ * place through their strides (HND or NHD; multiples of 8 elements, 16-byte
+ * aligned bases, key rows must not overlap); lse as in sage_attn_i8_fwd_lse
+ * (NULL = not written).
+ * Replaces fp16_attn_t / bf16_attn_t (csrc/pybind_gfx11.cpp:24-31,
+ * csrc/attn_gfx11.h:21-39, csrc/attn_gfx11.cu:2275-2472; kernels :1465-1885);
+ * their bm_sel tile override has no counterpart (one tile shape on gfx950).
+ */
+int sage_attn_direct_fwd(const void* query, const void* key, const void* value_t, void* out, float* lse,
+                         int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                         int64_t q_len, int64_t kv_len, int64_t head_dim,
+                         int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                         int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                         int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                         int is_causal, double sm_scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -28,9 +28,16 @@ What it restates (all citations are paths in LuXuxue/sageattention-rdna3):
 * ``attn_i8_lse``          -- this build's real ``return_lse`` (the reference
                               returns zeros, ``sageattention/core.py:203-211``):
                               ln sum_j exp of the same scores, ln 2 * (m + log2 l)
-* ``sageattn``             -- ``sageattention/core.py:40-213`` (INT8 branch,
-                              fp32 -> fp16 ``:78-83``, default ``sm_scale``
-                              ``:65-66``, ``smooth_k`` default False ``:186``)
+* ``attn_direct``          -- ``csrc/attn_gfx11.cu:1465-1885,2275-2472`` (direct
+                              fp16/bf16 kernels: ``fl32(dot)*fl32(sm_scale*log2 e)``
+                              ``:1675``, masks ``:1676-1679``, the same softmax,
+                              fp16 P and ``out*(1/l)`` as the INT8 kernel)
+* ``use_direct_path``      -- ``sageattention/core.py:113-139`` (direct/INT8
+                              dispatch thresholds and their env overrides)
+* ``sageattn``             -- ``sageattention/core.py:40-213`` (dispatch, both
+                              branches, fp32 -> fp16 ``:78-83``, default
+                              ``sm_scale`` ``:65-66``, ``smooth_k`` default False
+                              ``:186``)
 
 Bit-exactness contract: quantised Q/K, their scales, the K mean and the V
 layout are defined here exactly (IEEE fp32, no contraction) and the HIP kernels
@@ -268,6 +275,35 @@ def _scores_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal):
     return s, hk
 
 
+def _softmax_pv(s, v_t, b, hk):
+    """Output rows (float64) from log2-domain scores s [rows, Sk] (masked = -inf), shared by both
+    kernels (INT8 csrc/attn_gfx11.cu:656-771, direct :1683-1805):
+        p_ij = exp2(s_ij - max_j s_ij), l_i = sum_j p_ij (unrounded)
+        o_i  = sum_j fp16(p_ij) * V_T[:, j] / l_i   (l_i == 0 -> 0)
+    """
+    Sk = s.shape[1]
+    vf = v_t[b, hk, :, :Sk].astype(np.float64).T
+    m = s.max(axis=1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    p = np.exp2(s - m)
+    l = p.sum(axis=1, keepdims=True)
+    p16 = p.astype(np.float16).astype(np.float64)
+    o = p16 @ vf
+    with np.errstate(invalid="ignore", divide="ignore"):
+        o = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
+    return o
+
+
+def _lse_from_scores(s):
+    """ln sum_j exp(s_ij * ln 2) = ln 2 * (m + log2 sum_j exp2(s_ij - m)) per row, -inf without a
+    live key."""
+    m = s.max(axis=1)
+    mf = np.where(np.isfinite(m), m, 0.0)
+    l = np.exp2(s - mf[:, None]).sum(axis=1)
+    with np.errstate(divide="ignore"):
+        return np.where(l > 0, (mf + np.log2(np.where(l > 0, l, 1.0))) * np.log(2.0), -np.inf)
+
+
 def attn_i8_rows(q8, k8, v_t, q_scale, k_scale, b, hq, rows, is_causal, n_kv_heads=None):
     """Attention output (float64, before the output cast) for selected rows of one head.
 
@@ -283,16 +319,7 @@ def attn_i8_rows(q8, k8, v_t, q_scale, k_scale, b, hq, rows, is_causal, n_kv_hea
     if Sk == 0 or rows.size == 0:
         return np.zeros((rows.size, D), np.float64)
     s, hk = _scores_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal)
-    vf = v_t[b, hk, :, :Sk].astype(np.float64).T
-    m = s.max(axis=1, keepdims=True)
-    m = np.where(np.isfinite(m), m, 0.0)
-    p = np.exp2(s - m)
-    l = p.sum(axis=1, keepdims=True)
-    p16 = p.astype(np.float16).astype(np.float64)
-    o = p16 @ vf
-    with np.errstate(invalid="ignore", divide="ignore"):
-        o = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
-    return o
+    return _softmax_pv(s, v_t, b, hk)
 
 
 def attn_i8_lse_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal):
@@ -307,11 +334,7 @@ def attn_i8_lse_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal):
     if Sk == 0 or rows.size == 0:
         return np.full(rows.size, -np.inf)
     s, _ = _scores_rows(q8, k8, q_scale, k_scale, b, hq, rows, is_causal)
-    m = s.max(axis=1)
-    mf = np.where(np.isfinite(m), m, 0.0)
-    l = np.exp2(s - mf[:, None]).sum(axis=1)
-    with np.errstate(divide="ignore"):
-        return np.where(l > 0, (mf + np.log2(np.where(l > 0, l, 1.0))) * np.log(2.0), -np.inf)
+    return _lse_from_scores(s)
 
 
 def attn_i8_lse(q8, k8, q_scale, k_scale, is_causal, row_block=512):
@@ -339,14 +362,103 @@ def attn_i8(q8, k8, v_t, q_scale, k_scale, is_causal, out_dtype, row_block=512):
 
 
 # --------------------------------------------------------------------------
+# direct (unquantised) attention
+# --------------------------------------------------------------------------
+def _direct_scores_rows(q32, k32, sm_scale, b, hq, rows, is_causal):
+    """log2-domain scores of the direct kernel (csrc/attn_gfx11.cu:1655-1680) for selected rows of
+    one head, float64, masked entries (j > i when causal, top-left) at -inf:
+        s_ij = fl32(fl32(q_i . k_j) * fl32(fl32(sm_scale) * log2 e))
+    q32/k32 are HND fp32 copies of the fp16/bf16 inputs (exact).  The dot product is accumulated
+    exactly (float64 over fp16/bf16 products) and rounded once to fp32; the kernels accumulate in
+    fp32 in a hardware order, a difference inside the tests' tolerance.  The reference masks with
+    -FLT_MAX/2 (:1677-1679): every masked p is 0 either way, because key 0 is live in every row.
+    GQA head map hkv = hq // (Hq/Hkv)."""
+    Hq = q32.shape[1]
+    Hkv = k32.shape[1]
+    Sk = k32.shape[2]
+    hk = hq // (Hq // Hkv)
+    acc = (q32[b, hq, rows].astype(np.float64) @ k32[b, hk].astype(np.float64).T).astype(np.float32)
+    s = (acc * sm_scale_log2e(sm_scale)).astype(np.float32).astype(np.float64)
+    if is_causal:
+        cols = np.arange(Sk)
+        s = np.where(cols[None, :] <= rows[:, None], s, -np.inf)
+    return s, hk
+
+
+def attn_direct_rows(q32, k32, v_t, sm_scale, b, hq, rows, is_causal):
+    """Direct-kernel output (float64, before the output cast) for selected rows of one head: the
+    scores of ``_direct_scores_rows`` through ``_softmax_pv`` (P fp16 for fp16 and bf16 inputs,
+    V_T fp16, csrc/attn_gfx11.cu:1465-1467,1683-1805)."""
+    Sk = k32.shape[2]
+    rows = np.asarray(rows, dtype=np.int64)
+    if Sk == 0 or rows.size == 0:
+        return np.zeros((rows.size, q32.shape[3]), np.float64)
+    s, hk = _direct_scores_rows(q32, k32, sm_scale, b, hq, rows, is_causal)
+    return _softmax_pv(s, v_t, b, hk)
+
+
+def attn_direct_lse_rows(q32, k32, sm_scale, b, hq, rows, is_causal):
+    """Log-sum-exp (float64, natural log) of the direct kernel's scores, as ``attn_i8_lse_rows``."""
+    Sk = k32.shape[2]
+    rows = np.asarray(rows, dtype=np.int64)
+    if Sk == 0 or rows.size == 0:
+        return np.full(rows.size, -np.inf)
+    s, _ = _direct_scores_rows(q32, k32, sm_scale, b, hq, rows, is_causal)
+    return _lse_from_scores(s)
+
+
+def attn_direct(q, k, v_t, dtype, layout, sm_scale, is_causal, row_block=512, lse=False):
+    """Full direct-kernel restatement (fp16_attn_t / bf16_attn_t, csrc/attn_gfx11.cu:2275-2472):
+    q, k in ``layout`` and ``dtype``, v_t from ``v_layout``; returns HND [B,Hq,Sq,D] in ``dtype``
+    (and the [B,Hq,Sq] float64 log-sum-exp when ``lse``)."""
+    q32 = to_f32(to_hnd(q, layout), dtype)
+    k32 = to_f32(to_hnd(k, layout), dtype)
+    B, Hq, Sq, D = q32.shape
+    out = np.zeros((B, Hq, Sq, D), np.float32)
+    lse_out = np.zeros((B, Hq, Sq), np.float64)
+    for b in range(B):
+        for h in range(Hq):
+            for r0 in range(0, Sq, row_block):
+                rows = np.arange(r0, min(Sq, r0 + row_block))
+                out[b, h, rows] = attn_direct_rows(q32, k32, v_t, sm_scale, b, h, rows, is_causal)
+                if lse:
+                    lse_out[b, h, rows] = attn_direct_lse_rows(q32, k32, sm_scale, b, h, rows, is_causal)
+    o = from_f32(out, dtype)
+    return (o, lse_out) if lse else o
+
+
+# --------------------------------------------------------------------------
 # whole path
 # --------------------------------------------------------------------------
-def sageattn(q, k, v, dtype, tensor_layout="HND", is_causal=False, sm_scale=None,
-             smooth_k=False, intermediates=False):
-    """``sageattention.core.sageattn`` INT8 branch (core.py:40-213).
+def use_direct_path(head_dim, q_len, kv_len, is_causal, tensor_layout, env=None):
+    """The reference's direct/INT8 dispatch (sageattention/core.py:113-139), thresholds overridable
+    through the same environment variables (``env`` defaults to ``os.environ``)."""
+    import os
 
-    Returns the output in the input layout and dtype (fp32 inputs go through
-    fp16, core.py:78-83,200-201), optionally with the intermediates dict.
+    env = os.environ if env is None else env
+
+    def thr(name, default):
+        return int(env.get(name, str(default)) or default)
+
+    if head_dim == 64:
+        if is_causal:
+            return kv_len <= thr("SAGEATTN_DIRECT_THRESHOLD_D64_CAUSAL", 6144)
+        if q_len < kv_len:
+            return kv_len <= thr("SAGEATTN_DIRECT_THRESHOLD_D64_CROSS", 6144)
+        return kv_len <= thr("SAGEATTN_DIRECT_THRESHOLD_D64", 2048 if tensor_layout == "HND" else 3072)
+    if q_len * 2 < kv_len:
+        return kv_len <= thr("SAGEATTN_DIRECT_THRESHOLD_D128_CROSS", 4096)
+    return kv_len <= thr("SAGEATTN_DIRECT_THRESHOLD_D128", 2048)
+
+
+def sageattn(q, k, v, dtype, tensor_layout="HND", is_causal=False, sm_scale=None,
+             smooth_k=False, intermediates=False, path="auto", lse=False):
+    """``sageattention.core.sageattn`` (core.py:40-213): the direct branch or the INT8 branch.
+
+    ``path``: "auto" (the reference's dispatch, ``use_direct_path``), "int8" or "direct".
+    Returns the output in the input layout and dtype (fp32 inputs go through fp16,
+    core.py:78-83,200-201), then the [B,Hq,Sq] log-sum-exp when ``lse``, then the intermediates
+    dict when ``intermediates`` (its "path" names the branch taken).
     """
     D = q.shape[-1]
     if sm_scale is None:
@@ -355,18 +467,31 @@ def sageattn(q, k, v, dtype, tensor_layout="HND", is_causal=False, sm_scale=None
     if dtype == F32:
         q, k, v = (np.asarray(t, np.float32).astype(np.float16) for t in (q, k, v))
         dtype = F16
-    mean = k_mean(k, dtype, tensor_layout) if smooth_k else None
-    q8, qs, k8, ks = quant_qk_int8(q, k, dtype, tensor_layout, sm_scale, mean)
+    sq_axis = 2 if tensor_layout == "HND" else 1
+    Sq, Sk = q.shape[sq_axis], k.shape[sq_axis]
+    if path == "auto":
+        path = "direct" if use_direct_path(D, Sq, Sk, is_causal, tensor_layout) else "int8"
     vt = v_layout(v, dtype, tensor_layout)
-    o = attn_i8(q8, k8, vt, qs, ks, is_causal, dtype)
+    if path == "direct":
+        o, lse_v = attn_direct(q, k, vt, dtype, tensor_layout, sm_scale, is_causal, lse=True)
+        inter = dict(path="direct", v_t=vt)
+    else:
+        mean = k_mean(k, dtype, tensor_layout) if smooth_k else None
+        q8, qs, k8, ks = quant_qk_int8(q, k, dtype, tensor_layout, sm_scale, mean)
+        o = attn_i8(q8, k8, vt, qs, ks, is_causal, dtype)
+        lse_v = attn_i8_lse(q8, k8, qs, ks, is_causal) if lse else None
+        inter = dict(path="int8", mean=mean, q8=q8, q_scale=qs, k8=k8, k_scale=ks, v_t=vt)
     if tensor_layout == "NHD":
         o = o.transpose(0, 2, 1, 3)
     o = np.ascontiguousarray(o)
     if in_dtype == F32:
         o = o.astype(np.float32)
+    res = (o,)
+    if lse:
+        res += (lse_v,)
     if intermediates:
-        return o, dict(mean=mean, q8=q8, q_scale=qs, k8=k8, k_scale=ks, v_t=vt)
-    return o
+        res += (inter,)
+    return res[0] if len(res) == 1 else res
 
 
 def attn_ops(B, Hq, Sq, Sk, D, is_causal):

@@ -47,7 +47,7 @@ SOURCES = [
     ("prologue.hip", ["-ffp-contract=off"]),
     # MFMA results in arch VGPRs: the softmax reads every S element and the
     # rare O rescale touches O; AGPR residency costs v_accvgpr copies per tile
-    ("attn_i8.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    ("attn.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
 ]
 
 

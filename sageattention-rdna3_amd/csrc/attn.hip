@@ -1,18 +1,23 @@
-// Fused INT8-QK^T / fp16-PV flash attention for gfx950 (CDNA4, wave64 MFMA).
+// Fused flash attention for gfx950 (CDNA4, wave64 MFMA): the INT8 quantized
+// path and the direct fp16/bf16 path, one kernel template.
 //
-// Math (csrc/attn_gfx11.cu:409-825 of the reference): for query row i and key j
-//   s_ij = float(sum_d q8[i,d] * k8[j,d]) * (q_scale[i/32] * k_scale[j/16])
-// (log2 domain: Q was pre-scaled by sm_scale*log2 e), causal mask j > i
-// (top-left) and j >= Sk, online softmax with exp2, P rounded to fp16 (RNE),
-// O += P.V with fp32 accumulation, out = O * (1/l) cast to fp16/bf16.
+// Math (csrc/attn_gfx11.cu of the reference):
+//   INT8   (:409-825)   s_ij = float(sum_d q8[i,d] * k8[j,d]) * (q_scale[i/32] * k_scale[j/16])
+//   direct (:1465-1885) s_ij = fp32(sum_d q[i,d] * k[j,d]) * fl(sm_scale * log2 e)  (fp16 or bf16 Q/K)
+// in the log2 domain (INT8: Q was pre-scaled by sm_scale*log2 e), causal mask
+// j > i (top-left) and j >= Sk, online softmax with exp2, P rounded to fp16
+// (RNE), O += P.V_T with fp32 accumulation (V_T fp16 in both paths), out =
+// O * (1/l) cast to fp16/bf16.
 //
 // Mapping onto CDNA4:
 //   * block = 8 waves x 32 query rows (BM = 256), one block per CU, two waves
 //     per SIMD; KV tiles of BN = 64 keys shared by all 8 waves through LDS;
-//   * S^T = K . Q^T with v_mfma_i32_32x32x32_i8: A = K rows from LDS, B = the
-//     wave's Q^T fragment held in registers for the whole kernel.  The 32x32
-//     accumulator puts one query per lane column (lane & 31), so the row
-//     softmax is 32 in-lane values plus one permlane32 swap;
+//   * S^T = K . Q^T: A = K rows from LDS, B = the wave's Q^T fragment held in
+//     registers for the whole kernel (v_mfma_i32_32x32x32_i8, or
+//     v_mfma_f32_32x32x16_f16/bf16 for the direct path: both take 32 bytes of
+//     each row per MFMA).  The 32x32 accumulator puts one query per lane
+//     column (lane & 31), so the row softmax is 32 in-lane values plus one
+//     permlane32 swap;
 //   * O^T = V^T . P^T with v_mfma_f32_32x32x16_f16: B = P^T taken straight
 //     from the S^T accumulators (no LDS round trip), A = V_T rows from LDS.
 //     K rows sit in LDS with bits 2 and 3 of the key index swapped, which
@@ -30,7 +35,8 @@
 //     step, after the P.V MFMAs that still used the old max;
 //   * K/V tiles stream into a 3-stage LDS ring with buffer_load ... lds
 //     (no staging registers), issued two steps ahead; loads past the block's
-//     last key read as zero through the descriptor's record count;
+//     last key read as zero through the descriptor's record count.  The
+//     direct path reads K (and Q) straight from the caller's strided tensors;
 //   * causal: the KV loop stops at the block's last row, masks only on tail /
 //     diagonal tiles;
 //   * block -> work remap keeps consecutive q-blocks of a head on one XCD
@@ -52,16 +58,27 @@ constexpr int kXcds = 8;                   // MI355X: workgroups are dealt round
 constexpr float kRescale = 8.0f;           // lazy-rescale threshold of the running max (log2 units)
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (raw dword access)
 
+// Q/K operand kinds
+constexpr int kQkI8 = 0;    // INT8 Q/K (quantized path), per-block scales
+constexpr int kQkF16 = 1;   // fp16 Q/K (direct path)
+constexpr int kQkBf16 = 2;  // bf16 Q/K (direct path)
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
 struct AttnParams {
-  const int8_t* q8;      // [B,Hq,Sq,D]
-  const int8_t* k8;      // [B,Hkv,Sk,D]
+  const void* q;         // [B,Hq,Sq,D] (INT8: contiguous int8; direct: strided fp16/bf16)
+  const void* k;         // [B,Hkv,Sk,D] likewise
   const uint16_t* vt;    // fp16 [B,Hkv,D,np]
   void* out;
   float* lse;            // [B,Hq,Sq] or null
-  const float* q_scale;  // [B,Hq,ceil(Sq/32)]
-  const float* k_scale;  // [B,Hkv,ceil(Sk/16)]
+  const float* q_scale;  // [B,Hq,ceil(Sq/32)] (INT8 only)
+  const float* k_scale;  // [B,Hkv,ceil(Sk/16)] (INT8 only)
+  int64_t q_sb, q_sh, q_sn;  // Q/K strides in elements
+  int64_t k_sb, k_sh, k_sn;
   int64_t o_sb, o_sh, o_sn;
   int64_t np;
+  float sc;              // direct path: |fl(sm_scale * log2 e)|
+  uint32_t q_xor;        // direct path: 0x80008000 negates Q (sm_scale < 0), else 0
   int32_t hq, hkv, sq, sk;
   int32_t group;         // Hq / Hkv
   int32_t nqb;           // query blocks per head
@@ -69,10 +86,11 @@ struct AttnParams {
   int32_t work;          // B * Hq * nqb
 };
 
-template <int D>
+template <int D, int QK>
 struct Cfg {
+  static constexpr int kElem = QK == kQkI8 ? 1 : 2;          // bytes per Q/K element
   static constexpr int kStages = 3;                          // LDS ring depth (K and V)
-  static constexpr int kKRow = D;                            // bytes per K row in LDS (unpadded)
+  static constexpr int kKRow = D * kElem;                    // bytes per K row in LDS (unpadded)
   static constexpr int kVRow = kBN * 2;                      // bytes per V_T row in LDS (unpadded)
   static constexpr int kKStage = kBN * kKRow;                // bytes of one K stage
   static constexpr int kVStage = D * kVRow;                  // bytes of one V stage
@@ -80,15 +98,17 @@ struct Cfg {
   static constexpr int kSmem = kStages * (kKStage + kVStage);
   static constexpr int kKLoads = kKStage / 1024;             // 1 KB LDS-direct loads per K tile
   static constexpr int kVLoads = kVStage / 1024;             // ... per V tile
+  static constexpr int kKPerWave = kKLoads >= kWaves ? kKLoads / kWaves : 1;  // waves < kKLoads only if fewer
   static constexpr int kVPerWave = kVLoads / kWaves;
-  // loads every wave issues per step (waves 0..kKLoads-1 issue one more when
-  // a K tile has fewer 1 KB pieces than there are waves); waiting until at
-  // most this many are in flight retires everything issued a step earlier
-  static constexpr int kStepLoads = kVPerWave + (kKLoads >= kWaves ? 1 : 0);
-  static constexpr int kDS = D / 32;                         // k-steps of the QK MFMA
+  // loads every wave issues per step (when a K tile has fewer 1 KB pieces than
+  // there are waves, waves 0..kKLoads-1 issue one more); waiting until at most
+  // this many are in flight retires everything issued a step earlier
+  static constexpr int kStepLoads = kVPerWave + (kKLoads >= kWaves ? kKPerWave : 0);
+  static constexpr int kDS = kKRow / 32;                     // k-steps of the QK MFMA (32 bytes of a row each)
   static constexpr int kDB = D / 32;                         // 32-row d blocks of O^T
+  using SAcc = std::conditional_t<QK == kQkI8, int16_t_, float16_t_>;  // S^T accumulator block
   static_assert(kVLoads % kWaves == 0, "V tile must split evenly over the waves");
-  static_assert(kKLoads == kWaves || kKLoads < kWaves, "at most one K piece per wave");
+  static_assert(kKLoads < kWaves || kKLoads % kWaves == 0, "K tile must split evenly over the waves");
 };
 
 // LDS tiles are unpadded rows of 16-byte chunks; chunk c of row r is stored at
@@ -100,7 +120,7 @@ struct Cfg {
 // same function maps position -> chunk for the loads.
 template <int ROW_BYTES>
 __device__ __forceinline__ int swz(int row) {
-  static_assert(ROW_BYTES == 128 || ROW_BYTES == 64, "rows of 4 or 8 chunks");
+  static_assert(ROW_BYTES == 256 || ROW_BYTES == 128 || ROW_BYTES == 64, "rows of 4, 8 or 16 chunks");
   constexpr int kRowsPerWindow = 256 / ROW_BYTES;
   constexpr int kChunks = ROW_BYTES / 16;
   return (row / kRowsPerWindow) & (kChunks - 1);
@@ -142,10 +162,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // One 16-byte-per-lane buffer load straight into LDS (buffer_load_dwordx4
 // ... lds): the wave's 64 lanes fill 1 KB at `lds_dst` + lane*16 from byte
 // voffset + soffset of the buffer; lanes past the descriptor's end write
-// zeros.  The builtin takes an
-// LDS-address-space pointer, which only the device pass of this single-source
-// file can form; in the host pass (which compiles no device code but would
-// otherwise drop the kernels' launch stubs) the body is empty.
+// zeros.  The builtin takes an LDS-address-space pointer, which only the
+// device pass of this single-source file can form; in the host pass (which
+// compiles no device code but would otherwise drop the kernels' launch stubs)
+// the body is empty.
 __device__ __forceinline__ void lds_direct_load16(__amdgpu_buffer_rsrc_t rsrc, char* lds_dst, uint32_t voffset,
                                                   uint32_t soffset) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -160,23 +180,25 @@ __device__ __forceinline__ void lds_direct_load16(__amdgpu_buffer_rsrc_t rsrc, c
 // fills 1 KB of LDS at M0 + lane*16, so a lane's source offset picks the
 // chunk that belongs at its LDS position (inverse swizzle; K rows also go
 // through kperm).  One descriptor per head and tensor, the tile's position in
-// the scalar offset: K ends at the block's last key (kv_end), so tiles and
-// rows past it read as zero without touching memory; V_T ends at its padded
-// row end (tiles past kv_end are loaded but never used).
-template <int D>
+// the scalar offset: K ends just after the block's last key row (kv_end), so
+// tiles and rows past it read as zero without touching memory; V_T ends at its
+// padded row end (tiles past kv_end are loaded but never used).
+template <int D, int QK>
 struct TileLoader {
-  using C = Cfg<D>;
-  uint32_t k_goff;                 // this lane's byte offset in the K tile
+  using C = Cfg<D, QK>;
+  uint32_t k_goff[C::kKPerWave];   // this lane's byte offsets in the K tile (row pitch k_pitch)
   uint32_t v_goff[C::kVPerWave];   // ... in the V_T tile (row pitch np)
-  bool k_wave;                     // this wave loads one 1 KB piece of K
+  bool k_wave;                     // this wave loads K pieces
+  int k_pitch;                     // bytes between K rows in global memory
 
-  __device__ __forceinline__ TileLoader(int wave, int lane, int np) {
-    k_wave = wave < C::kKLoads;
-    {
-      const int byte = wave * 1024 + lane * 16;  // LDS byte in the K stage
+  __device__ __forceinline__ TileLoader(int wave, int lane, int np, int k_pitch_) : k_pitch(k_pitch_) {
+    k_wave = C::kKLoads >= kWaves || wave < C::kKLoads;
+#pragma unroll
+    for (int i = 0; i < C::kKPerWave; ++i) {
+      const int byte = (wave * C::kKPerWave + i) * 1024 + lane * 16;  // LDS byte in the K stage
       const int row = byte / C::kKRow;
       const int c = ((byte % C::kKRow) / 16) ^ swz<C::kKRow>(row);
-      k_goff = kperm(row) * D + c * 16;
+      k_goff[i] = static_cast<uint32_t>(kperm(row) * k_pitch + c * 16);
     }
 #pragma unroll
     for (int i = 0; i < C::kVPerWave; ++i) {
@@ -187,10 +209,14 @@ struct TileLoader {
     }
   }
 
-  // K rows kt.. through the head's K descriptor rk (rows past the block's
-  // last key read as zero) into the K stage at kstage.
+  // K rows kt.. through the head's K descriptor rk into the K stage at kstage.
   __device__ __forceinline__ void issue_k(__amdgpu_buffer_rsrc_t rk, char* kstage, int kt, int wave) const {
-    if (k_wave) lds_direct_load16(rk, kstage + wave * 1024, k_goff, static_cast<uint32_t>(kt * D));
+    if (k_wave) {
+#pragma unroll
+      for (int i = 0; i < C::kKPerWave; ++i)
+        lds_direct_load16(rk, kstage + (wave * C::kKPerWave + i) * 1024, k_goff[i],
+                          static_cast<uint32_t>(kt * k_pitch));
+    }
   }
   // V_T tokens kt.. through the head's V_T descriptor rv into the V stage at vstage.
   __device__ __forceinline__ void issue_v(__amdgpu_buffer_rsrc_t rv, char* vstage, int kt, int wave) const {
@@ -208,17 +234,23 @@ __device__ __forceinline__ void wait_loads_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// The tile's 4 key-group scales, read through the constant address space so
-// they land in SGPRs (the address is wave-uniform and nothing writes the
-// scales during the kernel); groups past the end repeat the last one and only
-// meet masked keys.
+// The tile's 4 key-group scales (INT8 path), read through the constant address
+// space so they land in SGPRs (the address is wave-uniform and nothing writes
+// the scales during the kernel); groups past the end repeat the last one and
+// only meet masked keys.  The direct path's scale is one constant.
 typedef const __attribute__((address_space(4))) float* const_f32_ptr;
+template <int QK>
 __device__ __forceinline__ void load_ks(const AttnParams& p, const float* ksp, int kt, float (&ks)[4]) {
-  const_f32_ptr kc = (const_f32_ptr)(reinterpret_cast<uint64_t>(uniform_ptr(ksp)));
+  if constexpr (QK == kQkI8) {
+    const_f32_ptr kc = (const_f32_ptr)(reinterpret_cast<uint64_t>(uniform_ptr(ksp)));
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int gi = kt / 16 + g;
-    ks[g] = kc[gi < p.k_groups ? gi : p.k_groups - 1];
+    for (int g = 0; g < 4; ++g) {
+      const int gi = kt / 16 + g;
+      ks[g] = kc[gi < p.k_groups ? gi : p.k_groups - 1];
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) ks[g] = 1.0f;
   }
 }
 
@@ -227,9 +259,9 @@ __device__ __forceinline__ void load_ks(const AttnParams& p, const float* ksp, i
 // same swizzle (32 is a multiple of the swizzle period).  The K offsets carry
 // the K ring's base, so that stage and block offsets (< 64 KB) fold into the
 // ds_read immediate.
-template <int D>
+template <int D, int QK>
 struct OperandMap {
-  using C = Cfg<D>;
+  using C = Cfg<D, QK>;
   uint32_t k_off[C::kDS];
   uint32_t v_off[4];
   __device__ __forceinline__ OperandMap(int m, int hh) {
@@ -241,8 +273,23 @@ struct OperandMap {
   }
 };
 
+// One QK MFMA: S^T block += K rows (a) . Q^T fragment (b), 32 bytes of each row.
+template <int QK>
+__device__ __forceinline__ typename Cfg<64, QK>::SAcc qk_mfma(int4_t a, int4_t b, const typename Cfg<64, QK>::SAcc& c,
+                                                              bool first) {
+  if constexpr (QK == kQkI8) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, first ? int16_t_{} : c, 0, 0, 0);
+  } else if constexpr (QK == kQkF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b),
+                                                  first ? float16_t_{} : c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   first ? float16_t_{} : c, 0, 0, 0);
+  }
+}
+
 // Softmax of one tile for one wave, cut into pieces that the pipelined step
-// spreads between its MFMAs: S (int32 accumulators, read only) -> P (fp16
+// spreads between its MFMAs: S (accumulators, read only) -> P (fp16
 // fragments), running max and sum.  O is not touched: when the reference max
 // moves (need), alpha = exp2(m_old - m_new) is left for the caller to apply to
 // O before the next P.V.  On masked tiles the dead keys (j >= Sk, causal
@@ -251,17 +298,23 @@ struct OperandMap {
 // step t = i/4, registers 8(t%2) + 2(i%4) .. +1 of block t/2), each in three
 // stages that the step places in consecutive chunks, so the exp latency of one
 // pair hides behind the work of its neighbours:
-//   pieces 0-3     integer max of key group g, scaled (group g = step g)
+//   pieces 0-3     max of key group g, scaled (group g = step g)
 //   piece  4       row max, lazy reference max, alpha
 //   pieces 5-20    A(i): y = acc*sc - m_run (dequant and max in one FMA)
 //   pieces 21-36   B(i): e = exp2(y)
 //   pieces 37-52   C(i): fp16 RNE pair into the P^T fragment, partial sums
 //   piece  53      l = l*alpha + sums
-template <int D, bool CAUSAL, bool MASK>
+// Scales: INT8 fl(q_scale * k_scale) per 16-key group; direct fl(sm_scale *
+// log2 e) for all keys.  x -> x*sc is monotonic for sc > 0, so the group max
+// can be taken on the raw accumulators: as int32 for INT8 (dead keys count as
+// INT32_MIN, which no real dot product reaches: |acc| <= 128*128*D < 2^22), as
+// fp32 for the direct path (dead keys -inf).
+template <int D, int QK, bool CAUSAL, bool MASK>
 struct TileSoftmax {
   static constexpr int kPieces = 54;
+  using SAcc = typename Cfg<D, QK>::SAcc;
   const AttnParams& p;
-  const int16_t_ (&acc)[2];
+  const SAcc (&acc)[2];
   const float (&ks)[4];
   float qs;
   int kt, qrow, hh;
@@ -272,8 +325,8 @@ struct TileSoftmax {
   float lsum[2];
   uint32_t w[4][4];
 
-  __device__ __forceinline__ TileSoftmax(const AttnParams& p_, const int16_t_ (&acc_)[2], const float (&ks_)[4],
-                                         float qs_, int kt_, int qrow_, int hh_)
+  __device__ __forceinline__ TileSoftmax(const AttnParams& p_, const SAcc (&acc_)[2], const float (&ks_)[4], float qs_,
+                                         int kt_, int qrow_, int hh_)
       : p(p_), acc(acc_), ks(ks_), qs(qs_), kt(kt_), qrow(qrow_), hh(hh_) {
     lsum[0] = lsum[1] = 0.0f;
   }
@@ -287,21 +340,30 @@ struct TileSoftmax {
   template <int K>
   __device__ __forceinline__ void piece(float& m_run, float& l_run, float& alpha, bool& need, half8_t (&pf)[4]) {
     if constexpr (K < 4) {
-      // dequant scale fl(q_scale * k_scale) and the group's integer max: x ->
-      // x*sc is monotonic for sc > 0, so this is max_j fl(acc*sc); dead keys
-      // count as INT32_MIN, which no real dot product reaches (|acc| <=
-      // 128*128*D < 2^22)
       constexpr int g = K, nb = g >> 1;
-      sc[g] = qs * ks[g];
-      int gm = INT32_MIN;
+      sc[g] = QK == kQkI8 ? qs * ks[g] : p.sc;
+      if constexpr (QK == kQkI8) {
+        int gm = INT32_MIN;
 #pragma unroll
-      for (int r = (g & 1) * 8; r < (g & 1) * 8 + 8; ++r) {
-        int a = acc[nb][r];
-        if constexpr (MASK) a = dead(nb, r) ? INT32_MIN : a;
-        gm = max(gm, a);
+        for (int r = (g & 1) * 8; r < (g & 1) * 8 + 8; ++r) {
+          int a = acc[nb][r];
+          if constexpr (MASK) a = dead(nb, r) ? INT32_MIN : a;
+          gm = max(gm, a);
+        }
+        gv[g] = static_cast<float>(gm) * sc[g];
+        if constexpr (MASK) gv[g] = (gm == INT32_MIN) ? -INFINITY : gv[g];
+      } else {
+        float gm = -INFINITY;
+#pragma unroll
+        for (int r = (g & 1) * 8; r < (g & 1) * 8 + 8; ++r) {
+          float a = acc[nb][r];
+          if constexpr (MASK) a = dead(nb, r) ? -INFINITY : a;
+          gm = __builtin_fmaxf(gm, a);
+        }
+        gv[g] = gm * sc[g];
+        // a group without a live key stays -inf (also for a zero scale)
+        if constexpr (MASK) gv[g] = (gm == -INFINITY) ? -INFINITY : gv[g];
       }
-      gv[g] = static_cast<float>(gm) * sc[g];
-      if constexpr (MASK) gv[g] = (gm == INT32_MIN) ? -INFINITY : gv[g];
     } else if constexpr (K == 4) {
       // lazy reference max: it moves only when some row's max grew by more
       // than kRescale (log2 units), so p = exp2(s - m_run) stays below
@@ -342,19 +404,19 @@ struct TileSoftmax {
 // alternate; lane half h supplies keys 16t + 8h .. 16t + 8h + 7), then the
 // QK MFMAs of the next tile, key block 0 before key block 1.  MFMA i reads its
 // A operand (16 bytes per lane) from LDS kAhead MFMAs earlier.
-template <int D>
+template <int D, int QK>
 struct StepMfma {
-  using C = Cfg<D>;
+  using C = Cfg<D, QK>;
   static constexpr int kPV = 4 * C::kDB;
   static constexpr int kQK = 2 * C::kDS;
   static constexpr int kN = kPV + kQK;
   static constexpr int kAhead = 2;
   const char* vst;
   const char* kst;
-  const OperandMap<D>& om;
+  const OperandMap<D, QK>& om;
   int4_t ring[kAhead + 1];
 
-  __device__ __forceinline__ StepMfma(const char* vst_, const char* kst_, const OperandMap<D>& om_)
+  __device__ __forceinline__ StepMfma(const char* vst_, const char* kst_, const OperandMap<D, QK>& om_)
       : vst(vst_), kst(kst_), om(om_) {}
 
   template <int I>
@@ -369,19 +431,17 @@ struct StepMfma {
   }
   template <int I>
   __device__ __forceinline__ void mfma(const half8_t (&pf)[4], float16_t_ (&o)[C::kDB], const int4_t (&qf)[C::kDS],
-                                       int16_t_ (&acc)[2]) {
+                                       typename C::SAcc (&acc)[2]) {
     if constexpr (I < kPV) {
       constexpr int t = I / C::kDB, db = I % C::kDB;
       o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, ring[I % (kAhead + 1)]), pf[t], o[db],
                                                      0, 0, 0);
     } else {
       constexpr int q = I - kPV, nb = q / C::kDS, ds = q % C::kDS;
-      acc[nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ring[I % (kAhead + 1)], qf[ds], ds == 0 ? int16_t_{} : acc[nb],
-                                                      0, 0, 0);
+      acc[nb] = qk_mfma<QK>(ring[I % (kAhead + 1)], qf[ds], acc[nb], ds == 0);
     }
   }
 };
-
 
 // Softmax pieces of chunk c of a step (k-th of at most kMaxPieces; -1 =
 // none).  S and P are updated in place, so the order must respect: P^T
@@ -389,14 +449,15 @@ struct StepMfma {
 // that read it, and key block nb of S is read (group maxima, stage A) for the
 // last time before the first QK MFMA that overwrites it.  Stage A of pair i
 // needs the reference max of piece 4 (one chunk of slack for its ballot).
+// The QK MFMAs of key block 1 start at chunk 20 or later in every kind
+// (INT8 D=128: 16 P.V + 4 + 4; fp16/bf16 D=128: 16 + 8 + 8).
 constexpr int kMaxPieces = 6;
 template <int D>
 constexpr int chunk_piece(int c, int k) {
   int list[kMaxPieces] = {-1, -1, -1, -1, -1, -1};
   int n = 0;
   if constexpr (D == 128) {
-    // 24 MFMAs: P.V step t at 4t..4t+3, QK block 0 at 16-19, block 1 at 20-23;
-    // pair i: A in chunk i+4, B in i+5, C in i+6
+    // P.V step t at 4t..4t+3; pair i: A in chunk i+4, B in i+5, C in i+6
     if (c == 0) { list[n++] = 0; list[n++] = 1; }
     if (c == 1) { list[n++] = 2; list[n++] = 3; }
     if (c == 2) list[n++] = 4;
@@ -405,8 +466,9 @@ constexpr int chunk_piece(int c, int k) {
     if (c - 4 >= 0 && c - 4 < 16) list[n++] = 5 + c - 4;
     if (c == 22) list[n++] = 53;
   } else {
-    // 12 MFMAs: P.V step t at 2t, 2t+1, QK block 0 at 8-9, block 1 at 10-11;
-    // pairs 2q, 2q+1: A in chunk q+2, B in q+3, C in q+4
+    // P.V step t at 2t, 2t+1; QK block 0 from chunk 8, block 1 from chunk 10
+    // (INT8: 8 + 2 + 2) or 12 (fp16/bf16: 8 + 4 + 4); pairs 2q, 2q+1: A in
+    // chunk q+2, B in q+3, C in q+4
     if (c == 0) { list[n++] = 0; list[n++] = 1; list[n++] = 2; list[n++] = 3; }
     if (c == 1) list[n++] = 4;
     for (int u = 0; u < 2; ++u) {
@@ -433,12 +495,12 @@ __device__ __forceinline__ void run_piece(SM& sm, float& m_run, float& l_run, fl
 // One pipelined step: MFMA i, the operand read of MFMA i + kAhead and the
 // softmax pieces of chunk i, one chunk per MFMA; sched_barrier keeps the
 // chunks in this order, so the wave issues VALU work while each MFMA runs.
-template <int D, typename SM, int I>
-__device__ __forceinline__ void step_chunk(StepMfma<D>& mf, SM& sm, const half8_t (&p_prv)[4],
-                                           float16_t_ (&o)[Cfg<D>::kDB], const int4_t (&qf)[Cfg<D>::kDS],
-                                           int16_t_ (&s_nxt)[2], float& m_run, float& l_run, float& alpha, bool& need,
-                                           half8_t (&p_cur)[4]) {
-  mf.template read<I + StepMfma<D>::kAhead>();
+template <int D, int QK, typename SM, int I>
+__device__ __forceinline__ void step_chunk(StepMfma<D, QK>& mf, SM& sm, const half8_t (&p_prv)[4],
+                                           float16_t_ (&o)[Cfg<D, QK>::kDB], const int4_t (&qf)[Cfg<D, QK>::kDS],
+                                           typename Cfg<D, QK>::SAcc (&s_nxt)[2], float& m_run, float& l_run,
+                                           float& alpha, bool& need, half8_t (&p_cur)[4]) {
+  mf.template read<I + StepMfma<D, QK>::kAhead>();
   mf.template mfma<I>(p_prv, o, qf, s_nxt);
   run_piece<SM, chunk_piece<D>(I, 0)>(sm, m_run, l_run, alpha, need, p_cur);
   run_piece<SM, chunk_piece<D>(I, 1)>(sm, m_run, l_run, alpha, need, p_cur);
@@ -448,34 +510,35 @@ __device__ __forceinline__ void step_chunk(StepMfma<D>& mf, SM& sm, const half8_
   run_piece<SM, chunk_piece<D>(I, 5)>(sm, m_run, l_run, alpha, need, p_cur);
   __builtin_amdgcn_sched_barrier(0);
 }
-template <int D, typename SM, int... I>
-__device__ __forceinline__ void step_chunks(std::integer_sequence<int, I...>, StepMfma<D>& mf, SM& sm,
-                                            const half8_t (&p_prv)[4], float16_t_ (&o)[Cfg<D>::kDB],
-                                            const int4_t (&qf)[Cfg<D>::kDS], int16_t_ (&s_nxt)[2], float& m_run,
-                                            float& l_run, float& alpha, bool& need, half8_t (&p_cur)[4]) {
-  (step_chunk<D, SM, I>(mf, sm, p_prv, o, qf, s_nxt, m_run, l_run, alpha, need, p_cur), ...);
+template <int D, int QK, typename SM, int... I>
+__device__ __forceinline__ void step_chunks(std::integer_sequence<int, I...>, StepMfma<D, QK>& mf, SM& sm,
+                                            const half8_t (&p_prv)[4], float16_t_ (&o)[Cfg<D, QK>::kDB],
+                                            const int4_t (&qf)[Cfg<D, QK>::kDS],
+                                            typename Cfg<D, QK>::SAcc (&s_nxt)[2], float& m_run, float& l_run,
+                                            float& alpha, bool& need, half8_t (&p_cur)[4]) {
+  (step_chunk<D, QK, SM, I>(mf, sm, p_prv, o, qf, s_nxt, m_run, l_run, alpha, need, p_cur), ...);
 }
 
-// S^T of one 64-key tile for the wave's 32 queries (prologue only).
-template <int D>
-__device__ __forceinline__ void qk_tile(const char* kstage, const OperandMap<D>& om, const int4_t (&qf)[Cfg<D>::kDS],
-                                        int16_t_ (&acc)[2]) {
-  using C = Cfg<D>;
+// S^T of one 64-key tile for the wave's 32 queries (prologue and masked steps).
+template <int D, int QK>
+__device__ __forceinline__ void qk_tile(const char* kstage, const OperandMap<D, QK>& om,
+                                        const int4_t (&qf)[Cfg<D, QK>::kDS], typename Cfg<D, QK>::SAcc (&acc)[2]) {
+  using C = Cfg<D, QK>;
 #pragma unroll
   for (int ds = 0; ds < C::kDS; ++ds) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const int4_t a = *reinterpret_cast<const int4_t*>(kstage + nb * 32 * C::kKRow + om.k_off[ds]);
-      acc[nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[ds], ds == 0 ? int16_t_{} : acc[nb], 0, 0, 0);
+      acc[nb] = qk_mfma<QK>(a, qf[ds], acc[nb], ds == 0);
     }
   }
 }
 
-// O^T += V^T . P^T for one 64-key tile (the last tile only).
-template <int D>
-__device__ __forceinline__ void pv_tile(const char* vstage, const OperandMap<D>& om, const half8_t (&pf)[4],
-                                        float16_t_ (&o)[Cfg<D>::kDB]) {
-  using C = Cfg<D>;
+// O^T += V^T . P^T for one 64-key tile (the last tile and masked steps).
+template <int D, int QK>
+__device__ __forceinline__ void pv_tile(const char* vstage, const OperandMap<D, QK>& om, const half8_t (&pf)[4],
+                                        float16_t_ (&o)[Cfg<D, QK>::kDB]) {
+  using C = Cfg<D, QK>;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
 #pragma unroll
@@ -486,9 +549,10 @@ __device__ __forceinline__ void pv_tile(const char* vstage, const OperandMap<D>&
   }
 }
 
-template <int D, bool CAUSAL, bool OUT_BF16>
-__global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
-  using C = Cfg<D>;
+template <int D, int QK, bool CAUSAL, bool OUT_BF16>
+__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
+  using C = Cfg<D, QK>;
+  using SAcc = typename C::SAcc;
   __shared__ __align__(16) char smem[C::kSmem];
 
   // ---- work decode: XCD-contiguous ranges, heaviest causal blocks first
@@ -513,10 +577,14 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   const int wrow0 = q0 + wave * 32;
   const int qrow = wrow0 + m;
 
-  // ---- Q^T fragments and the wave's q scale
+  // ---- Q^T fragments (lane (m, hh): bytes 32x + 16hh of row qrow for k-step
+  // x) and the wave's q scale
   int4_t qf[C::kDS];
   {
-    const int8_t* qp = p.q8 + (static_cast<int64_t>(bh) * p.sq + qrow) * D + hh * 16;
+    const char* qp = static_cast<const char*>(p.q) + hh * 16 +
+                     (QK == kQkI8 ? (static_cast<int64_t>(bh) * p.sq + qrow) * D
+                                  : (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq) * p.q_sh +
+                                     static_cast<int64_t>(qrow) * p.q_sn) * C::kElem);
 #pragma unroll
     for (int ds = 0; ds < C::kDS; ++ds) {
       if (qrow < p.sq) {
@@ -524,14 +592,21 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
       } else {
         qf[ds] = int4_t{0, 0, 0, 0};
       }
+      // a negative scale goes into Q's sign bits (exact), so the scale the
+      // softmax sees is positive and max commutes with it
+      if constexpr (QK != kQkI8) qf[ds] ^= static_cast<int>(p.q_xor);
     }
   }
-  const float qs = (wrow0 < p.sq) ? p.q_scale[static_cast<int64_t>(bh) * p.q_groups + wrow0 / 32] : 0.0f;
+  float qs = 1.0f;
+  if constexpr (QK == kQkI8) qs = (wrow0 < p.sq) ? p.q_scale[static_cast<int64_t>(bh) * p.q_groups + wrow0 / 32] : 0.0f;
 
   const int64_t bhk = static_cast<int64_t>(b) * p.hkv + hk;
-  const int8_t* kbase = p.k8 + bhk * p.sk * D;
+  const char* kbase = static_cast<const char*>(p.k) + (QK == kQkI8 ? bhk * p.sk * D
+                                                                    : (static_cast<int64_t>(b) * p.k_sb + hk * p.k_sh) * C::kElem);
   const uint16_t* vbase = p.vt + bhk * D * p.np;
-  const float* ksp = p.k_scale + bhk * p.k_groups;
+  const float* ksp = QK == kQkI8 ? p.k_scale + bhk * p.k_groups : nullptr;
+  // INT8 K is the contiguous quant output: its row pitch is a constant
+  const int k_pitch = QK == kQkI8 ? D : static_cast<int>(p.k_sn) * C::kElem;
 
   const int kv_end = CAUSAL ? min(q0 + kBM, p.sk) : p.sk;
   const int ntiles = (kv_end + kBN - 1) / kBN;
@@ -549,16 +624,17 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   float l_run = 0.0f;
   float alpha = 1.0f;
   bool need = false;
-  int16_t_ s[2];     // S of the tile the next softmax reads
+  SAcc s[2];         // S of the tile the next softmax reads
   half8_t pf[4];     // P^T fragments of the tile the next P.V reads
 #pragma unroll
   for (int t = 0; t < 4; ++t) pf[t] = half8_t{};
   float ks[4];
 
-  const TileLoader<D> tl(wave, lane, static_cast<int>(p.np));
-  const auto rk = make_rsrc(kbase, static_cast<uint32_t>(kv_end * D));
+  const TileLoader<D, QK> tl(wave, lane, static_cast<int>(p.np), k_pitch);
+  // K: rows [0, kv_end) of the head; V_T: the head's padded rows
+  const auto rk = make_rsrc(kbase, kv_end > 0 ? static_cast<uint32_t>((kv_end - 1) * k_pitch + D * C::kElem) : 0u);
   const auto rv = make_rsrc(vbase, static_cast<uint32_t>(D * static_cast<int>(p.np) * 2));
-  const OperandMap<D> om(m, hh);
+  const OperandMap<D, QK> om(m, hh);
   char* const vring = smem;                // V stages, then K stages
   char* const kring = smem + C::kKBase;    // K stage base for the loads
   const char* const kread = smem;          // ... for operand reads (offsets carry kKBase)
@@ -585,8 +661,8 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
     wait_loads_barrier<0>();
     tl.issue_k(rk, kring + 2 * C::kKStage, 2 * kBN, wave);
     tl.issue_v(rv, vring + 0 * C::kVStage, 0, wave);
-    load_ks(p, ksp, 0, ks);
-    qk_tile<D>(kread, om, qf, s);
+    load_ks<QK>(p, ksp, 0, ks);
+    qk_tile<D, QK>(kread, om, qf, s);
 
     // Step j (stage index st = j % 3): wait for K_{j+1} and V_{j-1} (issued at
     // step j-2), apply the pending O rescale, issue K_{j+3} into stage j%3 and
@@ -608,19 +684,19 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
       tl.issue_k(rk, kring + st * C::kKStage, (j + 3) * kBN, wave);
       tl.issue_v(rv, vring + st1 * C::kVStage, (j + 1) * kBN, wave);
       if constexpr (!MASKED) {
-        using SM = TileSoftmax<D, CAUSAL, false>;
+        using SM = TileSoftmax<D, QK, CAUSAL, false>;
         SM sm(p, s, ks, qs, j * kBN, qrow, hh);
-        StepMfma<D> mf(vring + st2 * C::kVStage, kread + st1 * C::kKStage, om);
+        StepMfma<D, QK> mf(vring + st2 * C::kVStage, kread + st1 * C::kKStage, om);
         mf.template read<0>();
         mf.template read<1>();
-        step_chunks<D, SM>(std::make_integer_sequence<int, StepMfma<D>::kN>{}, mf, sm, pf, o, qf, s, m_run, l_run,
-                           alpha, need, pf);
+        step_chunks<D, QK, SM>(std::make_integer_sequence<int, StepMfma<D, QK>::kN>{}, mf, sm, pf, o, qf, s, m_run,
+                               l_run, alpha, need, pf);
       } else {
         // tail / diagonal tiles (a few per block): the same work in plain
         // order, P.V (reads P) -> softmax (reads S, writes P) -> QK (writes S)
-        pv_tile<D>(vring + st2 * C::kVStage, om, pf, o);
+        pv_tile<D, QK>(vring + st2 * C::kVStage, om, pf, o);
         auto softmax = [&](auto smask_tag) __attribute__((always_inline)) {
-          using SM = TileSoftmax<D, CAUSAL, decltype(smask_tag)::value>;
+          using SM = TileSoftmax<D, QK, CAUSAL, decltype(smask_tag)::value>;
           SM sm(p, s, ks, qs, j * kBN, qrow, hh);
           run_all_pieces(sm, std::make_integer_sequence<int, SM::kPieces>{}, m_run, l_run, alpha, need, pf);
         };
@@ -631,7 +707,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
         } else {
           softmax(std::true_type{});
         }
-        qk_tile<D>(kread + st1 * C::kKStage, om, qf, s);
+        qk_tile<D, QK>(kread + st1 * C::kKStage, om, qf, s);
       }
       // P_j and the row statistics are consumed a step later; pinning them
       // here keeps their computation in this step (otherwise it sinks past
@@ -640,7 +716,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
       // k scales of the next tile: issued here, after the step's last LDS
       // read, because a pending scalar load makes every later LDS wait a full
       // lgkmcnt(0) (scalar loads return out of order)
-      load_ks(p, ksp, (j + 1) * kBN, ks);
+      load_ks<QK>(p, ksp, (j + 1) * kBN, ks);
     };
     int j = 0, st = 0;
     for (; j + 3 <= n_main; j += 3) {
@@ -655,7 +731,7 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
     // last P.V: V_{ntiles-1} sits in stage (ntiles-1) % 3
     wait_loads_barrier<C::kStepLoads>();
     rescale_o();
-    pv_tile<D>(vring + (st == 0 ? 2 : st - 1) * C::kVStage, om, pf, o);
+    pv_tile<D, QK>(vring + (st == 0 ? 2 : st - 1) * C::kVStage, om, pf, o);
     // loads of tiles past the end may still be in flight into this block's LDS
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
@@ -691,29 +767,37 @@ __global__ __launch_bounds__(kThreads) void attn_i8_fwd_kernel(AttnParams p) {
   }
 }
 
-template <int D, bool CAUSAL>
+template <int D, int QK, bool CAUSAL>
 void launch(const AttnParams& p, bool out_bf16, hipStream_t st) {
   const dim3 grid(static_cast<uint32_t>(p.work)), block(kThreads);
   if (out_bf16) {
-    attn_i8_fwd_kernel<D, CAUSAL, true><<<grid, block, 0, st>>>(p);
+    attn_fwd_kernel<D, QK, CAUSAL, true><<<grid, block, 0, st>>>(p);
   } else {
-    attn_i8_fwd_kernel<D, CAUSAL, false><<<grid, block, 0, st>>>(p);
+    attn_fwd_kernel<D, QK, CAUSAL, false><<<grid, block, 0, st>>>(p);
   }
 }
 
-}  // namespace
-}  // namespace sage
+template <int QK>
+void launch_kind(const AttnParams& p, int64_t head_dim, bool causal, bool out_bf16, hipStream_t st) {
+  if (head_dim == 128) {
+    if (causal) launch<128, QK, true>(p, out_bf16, st);
+    else launch<128, QK, false>(p, out_bf16, st);
+  } else {
+    if (causal) launch<64, QK, true>(p, out_bf16, st);
+    else launch<64, QK, false>(p, out_bf16, st);
+  }
+}
 
-using namespace sage;
-
-namespace {
-
-int attn_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out, float* lse, const float* q_scale,
+// Validation and launch shared by the entry points.  Q/K strides are in
+// elements (INT8: the contiguous [B,H,N,D] of the quant outputs).
+int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* out, float* lse, const float* q_scale,
              const float* k_scale, int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t q_len,
-             int64_t kv_len, int64_t head_dim, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
-             int is_causal, void* stream, const char* fn) {
+             int64_t kv_len, int64_t head_dim, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
+             int64_t k_sn, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n, int is_causal, double sm_scale,
+             void* stream, const char* fn) {
   if (out_dtype != SAGE_DTYPE_F16 && out_dtype != SAGE_DTYPE_BF16)
-    return set_error(SAGE_ERR_INVALID_ARG, "out_dtype must be SAGE_DTYPE_F16 or SAGE_DTYPE_BF16, got %d", out_dtype);
+    return set_error(SAGE_ERR_INVALID_ARG, "%s: %s must be SAGE_DTYPE_F16 or SAGE_DTYPE_BF16, got %d", fn,
+                     qk == kQkI8 ? "out_dtype" : "dtype", out_dtype);
   if (head_dim != 64 && head_dim != 128)
     return set_error(SAGE_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld", static_cast<long long>(head_dim));
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || q_len < 0 || kv_len < 0)
@@ -722,10 +806,17 @@ int attn_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* 
     return set_error(SAGE_ERR_INVALID_ARG, "q_heads (%lld) must be a multiple of kv_heads (%lld)",
                      static_cast<long long>(q_heads), static_cast<long long>(kv_heads));
   if (batch == 0 || q_len == 0) return SAGE_OK;
-  if (!out || !q_i8 || !q_scale || (kv_len > 0 && (!k_i8 || !k_scale || !value_t)))
+  const bool i8 = qk == kQkI8;
+  if (!out || !q || (i8 && !q_scale) || (kv_len > 0 && (!k || !value_t || (i8 && !k_scale))))
     return set_error(SAGE_ERR_INVALID_ARG, "%s: null pointer argument", fn);
-  if (!aligned(q_i8, 16) || (kv_len > 0 && (!aligned(k_i8, 16) || !aligned(value_t, 16))))
-    return set_error(SAGE_ERR_ALIGNMENT, "%s: q_i8/k_i8/value_t must be 16-byte aligned", fn);
+  const int64_t elem = i8 ? 1 : 2;
+  if (!aligned(q, 16) || (kv_len > 0 && (!aligned(k, 16) || !aligned(value_t, 16))))
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: q/k/value_t must be 16-byte aligned", fn);
+  if (q_sb < 0 || q_sh < 0 || q_sn < 0 || k_sb < 0 || k_sh < 0 || k_sn < head_dim)
+    return set_error(SAGE_ERR_INVALID_ARG, "%s: q/k strides must be non-negative and K rows must not overlap", fn);
+  if (((q_sb * elem) % 16) || ((q_sh * elem) % 16) || ((q_sn * elem) % 16) || ((k_sb * elem) % 16) ||
+      ((k_sh * elem) % 16) || ((k_sn * elem) % 16))
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: q/k strides must be multiples of 16 bytes", fn);
   if (!aligned(out, 8) || (o_stride_b % 4) || (o_stride_h % 4) || (o_stride_n % 4))
     return set_error(SAGE_ERR_ALIGNMENT, "%s: out needs an 8-byte aligned base and strides that are multiples of 4", fn);
   if (lse != nullptr && !aligned(lse, 4))
@@ -733,22 +824,34 @@ int attn_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* 
   const int64_t nqb = cdiv(q_len, kBM);
   const int64_t work = batch * q_heads * nqb;
   const int64_t np = cdiv(kv_len, SAGE_VT_ALIGN) * SAGE_VT_ALIGN;
-  // per-head K and V_T are addressed through 32-bit buffer offsets
-  if (q_len > INT32_MAX - kBM || kv_len > INT32_MAX - kBN || work > INT32_MAX || head_dim * np * 2 > UINT32_MAX)
+  // per-head K and V_T are addressed through 32-bit buffer offsets (K tiles
+  // are fetched up to three tiles past the last one)
+  if (q_len > INT32_MAX - kBM || kv_len > INT32_MAX - kBN || work > INT32_MAX || head_dim * np * 2 > UINT32_MAX ||
+      (kv_len + kBN * 5) * k_sn * elem > UINT32_MAX)
     return set_error(SAGE_ERR_UNSUPPORTED, "%s: sizes beyond 32-bit limits", fn);
 
   AttnParams p;
-  p.q8 = q_i8;
-  p.k8 = k_i8;
+  p.q = q;
+  p.k = k;
   p.vt = static_cast<const uint16_t*>(value_t);
   p.out = out;
   p.lse = lse;
   p.q_scale = q_scale;
   p.k_scale = k_scale;
+  p.q_sb = q_sb;
+  p.q_sh = q_sh;
+  p.q_sn = q_sn;
+  p.k_sb = k_sb;
+  p.k_sh = k_sh;
+  p.k_sn = k_sn;
   p.o_sb = o_stride_b;
   p.o_sh = o_stride_h;
   p.o_sn = o_stride_n;
   p.np = np;
+  // as the reference: fl(fl(sm_scale) * log2 e); its sign moves into Q
+  const float sc = static_cast<float>(sm_scale) * 1.4426950408889634f;
+  p.sc = std::fabs(sc);
+  p.q_xor = std::signbit(sc) ? 0x80008000u : 0u;
   p.hq = static_cast<int32_t>(q_heads);
   p.hkv = static_cast<int32_t>(kv_heads);
   p.sq = static_cast<int32_t>(q_len);
@@ -760,17 +863,16 @@ int attn_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* 
   p.work = static_cast<int32_t>(work);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bf16 = out_dtype == SAGE_DTYPE_BF16;
-  if (head_dim == 128) {
-    if (is_causal) launch<128, true>(p, bf16, st);
-    else launch<128, false>(p, bf16, st);
-  } else {
-    if (is_causal) launch<64, true>(p, bf16, st);
-    else launch<64, false>(p, bf16, st);
-  }
+  if (qk == kQkI8) launch_kind<kQkI8>(p, head_dim, is_causal != 0, bf16, st);
+  else if (qk == kQkF16) launch_kind<kQkF16>(p, head_dim, is_causal != 0, bf16, st);
+  else launch_kind<kQkBf16>(p, head_dim, is_causal != 0, bf16, st);
   return check_launch(fn);
 }
 
 }  // namespace
+}  // namespace sage
+
+using namespace sage;
 
 extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
                                 const float* q_scale, const float* k_scale, int out_dtype,
@@ -779,8 +881,10 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
                                 int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                                 int is_causal, void* stream) {
   clear_error();
-  return attn_fwd(q_i8, k_i8, value_t, out, nullptr, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads, q_len,
-                  kv_len, head_dim, o_stride_b, o_stride_h, o_stride_n, is_causal, stream, "sage_attn_i8_fwd");
+  return attn_fwd(kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads,
+                  q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim, head_dim,
+                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
+                  is_causal, 0.0, stream, "sage_attn_i8_fwd");
 }
 
 extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
@@ -790,6 +894,22 @@ extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, cons
                                     int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                                     int is_causal, void* stream) {
   clear_error();
-  return attn_fwd(q_i8, k_i8, value_t, out, lse, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads, q_len,
-                  kv_len, head_dim, o_stride_b, o_stride_h, o_stride_n, is_causal, stream, "sage_attn_i8_fwd_lse");
+  return attn_fwd(kQkI8, q_i8, k_i8, value_t, out, lse, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads,
+                  q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim, head_dim,
+                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
+                  is_causal, 0.0, stream, "sage_attn_i8_fwd_lse");
+}
+
+extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const void* value_t, void* out, float* lse,
+                                    int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                    int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                                    int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                    int is_causal, double sm_scale, void* stream) {
+  clear_error();
+  return attn_fwd(dtype == SAGE_DTYPE_BF16 ? kQkBf16 : kQkF16, query, key, value_t, out, lse, nullptr, nullptr, dtype,
+                  batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b,
+                  k_stride_h, k_stride_n, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, stream,
+                  "sage_attn_direct_fwd");
 }

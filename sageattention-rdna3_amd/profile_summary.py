@@ -15,7 +15,7 @@ import json
 import sys
 
 COPY_BYTES = 1 << 30
-KERNELS = ("attn_i8_fwd_kernel", "quant_qk_i8_kernel", "v_layout_kernel", "k_mean_partial_kernel",
+KERNELS = ("attn_fwd_kernel", "quant_qk_i8_kernel", "v_layout_kernel", "k_mean_partial_kernel",
            "k_mean_final_kernel")
 
 
@@ -73,7 +73,9 @@ def traffic(fetch_csv, write_csv, out_json, out_md, command):
         fb = mean(fetch, k, "FETCH_SIZE") * f_scale
         wb = mean(write, k, "WRITE_SIZE") * w_scale
         res["kernels"][k] = {"fetch_bytes": fb, "write_bytes": wb, "bytes": fb + wb}
-    attn = [v for k, v in res["kernels"].items() if k.startswith("attn_i8_fwd_kernel")]
+    # attn_fwd_kernel<D, QK, CAUSAL, OUT_BF16>: QK 0 is the INT8 kernel
+    attn = [v for k, v in res["kernels"].items() if k.replace(" ", "").startswith(("attn_fwd_kernel<128,0,",
+                                                                                   "attn_fwd_kernel<64,0,"))]
     if attn:
         res["attn_bytes_per_launch"] = attn[0]["bytes"]
     json.dump(res, open(out_json, "w"), indent=1)

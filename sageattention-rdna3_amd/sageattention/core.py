@@ -1,14 +1,16 @@
-"""Drop-in ``sageattn`` for MI355X: the INT8 quantized path on gfx950 kernels.
+"""Drop-in ``sageattn`` for MI355X on gfx950 kernels.
 
 Mirrors ``sageattention/core.py:40-233`` of the reference (same signature,
-defaults, assertion messages, fp32 handling, ``smooth_k`` default False and
-the upstream alias); ``return_lse`` returns the real log-sum-exp where the
-reference returns a zero placeholder.  Every call takes the
-INT8 path; the reference's Triton backend, ``SAGEATTN_BACKEND`` switch and the
-direct fp16/bf16 branch (core.py:8,68-76,113-164) do not exist here.
+defaults, assertion messages, fp32 handling, ``smooth_k`` default False, the
+upstream alias and the direct/INT8 dispatch with its thresholds and
+``SAGEATTN_DIRECT_THRESHOLD_*`` environment overrides, core.py:113-139);
+``return_lse`` returns the real log-sum-exp where the reference returns a zero
+placeholder.  The reference's Triton backend and ``SAGEATTN_BACKEND`` switch
+(core.py:8,68-76) do not exist here.
 """
 from __future__ import annotations
 
+import os
 from typing import Any, Optional, Tuple, Union
 
 import torch
@@ -24,6 +26,32 @@ def _vector_ready(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous() if not t.is_contiguous() else t.clone()
 
 
+def _env_int(name: str, default: int) -> int:
+    return int(os.getenv(name, str(default)) or default)
+
+
+def use_direct_path(head_dim: int, q_len: int, kv_len: int, is_causal: bool, tensor_layout: str) -> bool:
+    """The reference's choice between the direct fp16/bf16 kernel (no
+    quantisation prologue) and the INT8 path (sageattention/core.py:113-139):
+    short key ranges go direct.  Defaults, per head_dim and shape:
+      D=64:  causal kv <= 6144; cross (q < kv) kv <= 6144; self kv <= 2048
+             (HND) or 3072 (NHD);
+      D=128: q * 2 < kv -> kv <= 4096; otherwise kv <= 2048.
+    Each threshold can be overridden by its environment variable
+    (SAGEATTN_DIRECT_THRESHOLD_D64[_CAUSAL|_CROSS], ..._D128[_CROSS]); a
+    negative value disables the direct path for that case."""
+    if head_dim == 64:
+        d64_default = 2048 if tensor_layout == "HND" else 3072
+        if is_causal:
+            return kv_len <= _env_int("SAGEATTN_DIRECT_THRESHOLD_D64_CAUSAL", 6144)
+        if q_len < kv_len:
+            return kv_len <= _env_int("SAGEATTN_DIRECT_THRESHOLD_D64_CROSS", 6144)
+        return kv_len <= _env_int("SAGEATTN_DIRECT_THRESHOLD_D64", d64_default)
+    if q_len * 2 < kv_len:
+        return kv_len <= _env_int("SAGEATTN_DIRECT_THRESHOLD_D128_CROSS", 4096)
+    return kv_len <= _env_int("SAGEATTN_DIRECT_THRESHOLD_D128", 2048)
+
+
 def sageattn(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -34,14 +62,17 @@ def sageattn(
     return_lse: bool = False,
     **kwargs: Any,
 ) -> Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]:
-    """Quantized attention: per-block INT8 Q/K (optional K-mean smoothing with
-    ``smooth_k=True``), fp16 V, fused INT8-QK^T / fp16-PV flash attention.
+    """SageAttention: per-block INT8 Q/K (optional K-mean smoothing with
+    ``smooth_k=True``), fp16 V, fused INT8-QK^T / fp16-PV flash attention; for
+    short key ranges (:func:`use_direct_path`) the direct kernel on the fp16 /
+    bf16 Q and K instead.
 
     q: [B,Hq,Sq,D] (HND) or [B,Sq,Hq,D] (NHD); k, v with Hkv heads (Hq % Hkv == 0).
     Returns o with q's shape, layout and dtype (and, when ``return_lse``, the
     rows' log-sum-exp [B,Hq,Sq] fp32: ln sum_j exp(sm_scale * q_i.k_j) after
     quantisation, -inf for a row with no key; the reference returns zeros).
-    Unknown kwargs are ignored.
+    ``bm_sel`` (the reference's experimental direct-kernel tile override) is
+    accepted and ignored; other unknown kwargs are ignored too.
     """
     dtype = q.dtype
     assert q.is_cuda, "Input tensors must be on CUDA/HIP device."
@@ -91,10 +122,22 @@ def sageattn(
     v = _vector_ready(v)
     o = torch.empty_like(q)
 
-    # V transform: fp16 V_T [B,Hkv,D,ceil64(Sk)] zero padded (core.py:171-180)
+    # V transform: fp16 V_T [B,Hkv,D,ceil64(Sk)] zero padded (core.py:145-152,171-180)
     padded_n = (Sk + 63) // 64 * 64
     v_t = torch.empty(B, Hkv, D, padded_n, device=q.device, dtype=torch.float16)
     ops.v_transpose(v, v_t, layout_code)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
+
+    if use_direct_path(D, Sq, Sk, bool(is_causal), tensor_layout):
+        # direct kernel reads Q and K in place (core.py:141-164); K rows must not overlap
+        k_token_stride = k.stride(2) if layout_code == ops.HND else k.stride(1)
+        if k_token_stride < D:
+            k = k.contiguous()
+        direct = ops.bf16_attn_t if input_dtype == torch.bfloat16 else ops.fp16_attn_t
+        direct(q, k, v_t, o, layout_code, int(is_causal), sm_scale, 0, lse=lse)
+        if input_dtype == torch.float32:
+            o = o.to(torch.float32)
+        return (o, lse) if return_lse else o
 
     smooth_k = kwargs.get("smooth_k", False)
     if smooth_k and Sk > 0:
@@ -104,7 +147,6 @@ def sageattn(
     q_int8, q_scale, k_int8, k_scale = ops.quant_qk_int8(q, k, k_mean, layout_code, sm_scale)
     # return_lse: the reference returns a zero placeholder (core.py:203-211); the fused kernel writes
     # the real log-sum-exp of each row (natural log, scaled scores; -inf for a row without keys)
-    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
     ops.qk_int8_sv_bf16_attn_t(q_int8, k_int8, v_t, o, q_scale, k_scale,
                                layout_code, int(is_causal), sm_scale, lse=lse)
 

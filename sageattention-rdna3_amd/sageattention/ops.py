@@ -142,3 +142,54 @@ def qk_int8_sv_bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.
                    _ptr(q_scale), _ptr(k_scale), _dtype_code(output),
                    B, Hq, Hkv, Sq, Sk, D, osb, osh, osn, int(bool(is_causal)), _stream(query))
     return output
+
+
+def _direct_attn_t(op: str, want: torch.dtype, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                   output: torch.Tensor, tensor_layout: int, is_causal: int, sm_scale: float,
+                   lse: Optional[torch.Tensor]) -> torch.Tensor:
+    for name, t in (("query", query), ("key", key), ("output", output)):
+        if t.dtype != want:
+            raise ValueError(f"{op}: {name} must be {want}, got {t.dtype}")
+        if t.dim() != 4 or t.stride(-1) != 1:
+            raise ValueError(f"{op}: {name} must be 4-D with a contiguous head_dim axis")
+    (B, Hq, Sq, D), (qsb, qsh, qsn) = _bhnd(query, tensor_layout)
+    (Bk, Hkv, Sk, Dk), (ksb, ksh, ksn) = _bhnd(key, tensor_layout)
+    if Bk != B or Dk != D:
+        raise ValueError(f"{op}: query {tuple(query.shape)} and key {tuple(key.shape)} disagree")
+    NP = (Sk + 63) // 64 * 64
+    if tuple(value.shape) != (B, Hkv, D, NP) or value.dtype != torch.float16 or not value.is_contiguous():
+        raise ValueError(f"{op}: value must be contiguous fp16 V_T [{B},{Hkv},{D},{NP}]")
+    (Bo, Ho, So, Do), (osb, osh, osn) = _bhnd(output, tensor_layout)
+    if (Bo, Ho, So, Do) != (B, Hq, Sq, D):
+        raise ValueError(f"{op}: output shape does not match the query")
+    lse_ptr = ctypes.c_void_p(0)
+    if lse is not None:
+        if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+            raise ValueError(f"{op}: lse must be contiguous fp32 [{B},{Hq},{Sq}]")
+        lse_ptr = _ptr(lse)
+    with torch.cuda.device(query.device):
+        _capi.call("sage_attn_direct_fwd", _ptr(query), _ptr(key), _ptr(value), _ptr(output), lse_ptr,
+                   _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, ksb, ksh, ksn, osb, osh, osn,
+                   int(bool(is_causal)), float(sm_scale), _stream(query))
+    return output
+
+
+def fp16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, output: torch.Tensor,
+                tensor_layout: int, is_causal: int, sm_scale: float, bm_sel: int = 0,
+                lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Direct attention on fp16 Q/K (no quantisation) and the fp16 V_T of
+    :func:`v_transpose` into fp16 ``output`` (reference fp16_attn_t,
+    csrc/attn_gfx11.cu:2275-2374).  ``bm_sel`` (the reference's experimental
+    tile override) is accepted and ignored: gfx950 uses one tile shape.
+    ``lse`` as in :func:`qk_int8_sv_bf16_attn_t`."""
+    return _direct_attn_t("fp16_attn_t", torch.float16, query, key, value, output, tensor_layout, is_causal,
+                          sm_scale, lse)
+
+
+def bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, output: torch.Tensor,
+                tensor_layout: int, is_causal: int, sm_scale: float, bm_sel: int = 0,
+                lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16 counterpart of :func:`fp16_attn_t`: bf16 Q/K/output, fp16 V_T and
+    P (reference bf16_attn_t, csrc/attn_gfx11.cu:2376-2472)."""
+    return _direct_attn_t("bf16_attn_t", torch.bfloat16, query, key, value, output, tensor_layout, is_causal,
+                          sm_scale, lse)

@@ -143,6 +143,45 @@ def test_attn_lse_zero_work_is_ok(lib):
     assert attn_lse(lib, B=0, lse=NULL) == _capi.OK
 
 
+def direct(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, vt=FAKE, o=FAKE, lse=NULL, dtype=1, B=1, Hq=4, Hkv=2, Sq=64, Sk=64, D=128,
+             qsb=4 * 64 * 128, qsh=64 * 128, qsn=128, ksb=2 * 64 * 128, ksh=64 * 128, ksn=128,
+             osb=4 * 64 * 128, osh=64 * 128, osn=128, causal=1, scale=0.125, stream=NULL)
+    a.update(kw)
+    return lib.sage_attn_direct_fwd(*a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        (dict(dtype=2), _capi.ERR_INVALID_ARG, "sage_attn_direct_fwd: dtype"),
+        (dict(D=256), _capi.ERR_UNSUPPORTED, "head_dim"),
+        (dict(Hq=3), _capi.ERR_INVALID_ARG, "multiple"),
+        (dict(Sk=-1), _capi.ERR_INVALID_ARG, "negative"),
+        (dict(k=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(o=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(q=ODD), _capi.ERR_ALIGNMENT, "aligned"),
+        (dict(vt=ODD), _capi.ERR_ALIGNMENT, "aligned"),
+        (dict(qsn=132), _capi.ERR_ALIGNMENT, "16 bytes"),
+        (dict(ksh=100), _capi.ERR_ALIGNMENT, "16 bytes"),
+        (dict(ksn=64), _capi.ERR_INVALID_ARG, "overlap"),
+        (dict(qsb=-8), _capi.ERR_INVALID_ARG, "non-negative"),
+        (dict(osn=130), _capi.ERR_ALIGNMENT, "strides"),
+        (dict(lse=ODD), _capi.ERR_ALIGNMENT, "lse"),
+        (dict(Sk=2 ** 24, ksn=2 ** 10), _capi.ERR_UNSUPPORTED, "32-bit"),
+    ],
+)
+def test_direct_validation(lib, kw, code, msg):
+    assert direct(lib, **kw) == code
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_direct_zero_work_is_ok(lib):
+    assert direct(lib, Sq=0) == _capi.OK
+    assert direct(lib, B=0, q=NULL) == _capi.OK
+    assert lib.sage_last_error() == b""
+
+
 def test_v_layout_and_mean_validation(lib):
     assert lib.sage_v_layout(FAKE, FAKE, 0, 1, 2, 100, 80, 0, 0, 0, NULL) == _capi.ERR_UNSUPPORTED
     assert lib.sage_v_layout(ODD, FAKE, 0, 1, 2, 100, 64, 0, 6400, 64, NULL) == _capi.ERR_ALIGNMENT

@@ -1,7 +1,9 @@
 """The reference's end-to-end test matrix (test_sageattn_rdna3.py:80-287, 36 cases),
-run through this build's ``sageattn`` -- which always takes the INT8 path -- and
-compared with fp32 SDPA (F.scaled_dot_product_attention on float32 copies) and
-with the CPU oracle of the same quantized math.
+run through this build's ``sageattn`` and compared with fp32 SDPA
+(F.scaled_dot_product_attention on float32 copies) and with the CPU oracle of
+the same math.  Every case runs twice: with the reference's direct/INT8
+dispatch ("auto": most of these short shapes take the direct kernel) and with
+the direct path switched off through its environment thresholds ("int8").
 
 Tolerances: the reference's own bands (cos > 0.99 fp16 / 0.98 bf16, max-abs <
 0.35, test_sageattn_rdna3.py:39-53) are kept as the outer bound and tightened
@@ -19,9 +21,26 @@ from _helpers import cos_sim, max_abs, np_to_f32, to_np
 pytestmark = pytest.mark.gpu
 
 
+DIRECT_ENV = ["SAGEATTN_DIRECT_THRESHOLD_D64", "SAGEATTN_DIRECT_THRESHOLD_D64_CAUSAL",
+              "SAGEATTN_DIRECT_THRESHOLD_D64_CROSS", "SAGEATTN_DIRECT_THRESHOLD_D128",
+              "SAGEATTN_DIRECT_THRESHOLD_D128_CROSS"]
+
+
 @pytest.fixture(autouse=True)
 def seed_random():
     torch.manual_seed(0)
+
+
+@pytest.fixture(autouse=True, params=["auto", "int8"])
+def dispatch(request, monkeypatch):
+    """"auto": the reference's default thresholds; "int8": every threshold -1 (no direct path).
+    The product and the oracle read the same environment."""
+    for name in DIRECT_ENV:
+        if request.param == "int8":
+            monkeypatch.setenv(name, "-1")
+        else:
+            monkeypatch.delenv(name, raising=False)
+    return request.param
 
 
 @pytest.fixture
@@ -49,7 +68,7 @@ def assert_close(out, ref, dtype, oracle=None):
     mae = max_abs(o, r)
     assert cos > (0.98 if dtype == torch.bfloat16 else 0.99), f"cosine similarity {cos} too low"
     assert mae < 0.35, f"Max abs error {mae} too high"
-    assert cos >= 0.999, f"INT8 path cos {cos} below 0.999"
+    assert cos >= 0.999, f"cos {cos} vs fp32 SDPA below 0.999"
     if oracle is not None:
         assert cos_sim(o, oracle) >= 0.99999
     return cos, mae
@@ -183,8 +202,7 @@ class TestApiContract:
         o, lse = sageattn(q, k, v, return_lse=True, is_causal=True)
         assert lse.shape == (2, 3, 100) and lse.dtype == torch.float32
         assert torch.equal(o, sageattn(q, k, v, is_causal=True))
-        _, inter = orc.sageattn(*(to_np(t) for t in (q, k, v)), "fp16", "HND", True, intermediates=True)
-        ref = orc.attn_i8_lse(inter["q8"], inter["k8"], inter["q_scale"], inter["k_scale"], True)
+        _, ref = orc.sageattn(*(to_np(t) for t in (q, k, v)), "fp16", "HND", True, lse=True)
         assert np.max(np.abs(to_np(lse).astype(np.float64) - ref)) < 2e-4
         qn = q.transpose(1, 2).contiguous()
         o2, lse2 = sageattn(qn, k.transpose(1, 2), v.transpose(1, 2), tensor_layout="NHD", return_lse=True,

@@ -276,40 +276,47 @@ def test_attention_matches_fp64_dequant_softmax(causal):
     assert cos_sim(o, ref) > 0.99999
 
 
-def test_attention_gqa_equals_repeated_heads():
+PATHS = ["int8", "direct"]
+
+
+@pytest.mark.parametrize("path", PATHS)
+def test_attention_gqa_equals_repeated_heads(path):
     rng = np.random.default_rng(8)
     q = rng.standard_normal((1, 4, 70, 64)).astype(np.float16)
     k = rng.standard_normal((1, 2, 70, 64)).astype(np.float16)
     v = rng.standard_normal((1, 2, 70, 64)).astype(np.float16)
-    o1 = orc.sageattn(q, k, v, "fp16", "HND", True)
-    o2 = orc.sageattn(q, np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1), "fp16", "HND", True)
+    o1 = orc.sageattn(q, k, v, "fp16", "HND", True, path=path)
+    o2 = orc.sageattn(q, np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1), "fp16", "HND", True, path=path)
     assert np.array_equal(o1, o2)
 
 
-def test_attention_nhd_equals_hnd():
+@pytest.mark.parametrize("path", PATHS)
+def test_attention_nhd_equals_hnd(path):
     rng = np.random.default_rng(9)
     q, k, v = (rng.standard_normal((2, 3, 90, 128)).astype(np.float16) for _ in range(3))
-    o1 = orc.sageattn(q, k, v, "fp16", "HND", True, smooth_k=True)
+    o1 = orc.sageattn(q, k, v, "fp16", "HND", True, smooth_k=True, path=path)
     t = lambda a: np.ascontiguousarray(a.transpose(0, 2, 1, 3))  # noqa: E731
-    o2 = orc.sageattn(t(q), t(k), t(v), "fp16", "NHD", True, smooth_k=True)
+    o2 = orc.sageattn(t(q), t(k), t(v), "fp16", "NHD", True, smooth_k=True, path=path)
     assert np.array_equal(o1, t(o2))
 
 
-def test_attention_single_key_and_first_causal_row():
+@pytest.mark.parametrize("path", PATHS)
+def test_attention_single_key_and_first_causal_row(path):
     rng = np.random.default_rng(10)
     q, k, v = (rng.standard_normal((1, 2, 1, 64)).astype(np.float16) for _ in range(3))
-    o = orc.sageattn(q, k, v, "fp16", "HND", False)
+    o = orc.sageattn(q, k, v, "fp16", "HND", False, path=path)
     assert np.array_equal(o, v)
     q, k, v = (rng.standard_normal((1, 2, 40, 64)).astype(np.float16) for _ in range(3))
-    o = orc.sageattn(q, k, v, "fp16", "HND", True)
+    o = orc.sageattn(q, k, v, "fp16", "HND", True, path=path)
     assert np.array_equal(o[:, :, 0], v[:, :, 0])
 
 
-def test_attention_constant_v_normalises():
+@pytest.mark.parametrize("path", PATHS)
+def test_attention_constant_v_normalises(path):
     rng = np.random.default_rng(11)
     q, k = (rng.standard_normal((1, 2, 100, 64)).astype(np.float16) for _ in range(2))
     v = np.full((1, 2, 100, 64), 0.5, np.float16)
-    o = orc.sageattn(q, k, v, "fp16", "HND", False).astype(np.float64)
+    o = orc.sageattn(q, k, v, "fp16", "HND", False, path=path).astype(np.float64)
     assert np.all(np.abs(o - 0.5) < 2e-3)
 
 
@@ -361,25 +368,139 @@ def test_attention_empty_kv_gives_zero():
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
 @pytest.mark.parametrize("causal", [False, True])
-def test_oracle_vs_fp32_sdpa(dtype, causal):
-    """Quantisation error budget of the algorithm itself (C1 shape)."""
+@pytest.mark.parametrize("path", PATHS)
+def test_oracle_vs_fp32_sdpa(dtype, causal, path):
+    """Error budget of each algorithm itself against fp32 SDPA (C1 shape): INT8 quantisation, or
+    for the direct path only the fp16 rounding of P and of the output (much tighter)."""
     cfg = Config("t", 1, 2, 2, 256, 64, dtype, "HND", causal, False)
     q, k, v = make_inputs(cfg, seed=3)
-    o = orc.sageattn(to_np(q), to_np(k), to_np(v), dtype, "HND", causal)
+    o = orc.sageattn(to_np(q), to_np(k), to_np(v), dtype, "HND", causal, path=path)
     o32 = orc.to_f32(o, "fp16" if dtype == "fp32" else dtype) if dtype != "fp32" else o
     ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=causal)
-    assert cos_sim(o32, ref.numpy()) > 0.999
-    assert max_abs(o32, ref.numpy()) < 0.05
+    if path == "int8":
+        assert cos_sim(o32, ref.numpy()) > 0.999
+        assert max_abs(o32, ref.numpy()) < 0.05
+    else:
+        assert cos_sim(o32, ref.numpy()) > 0.99999
+        assert max_abs(o32, ref.numpy()) < (1e-2 if dtype == "bf16" else 2e-3)
 
 
 def test_smooth_k_shift_invariance():
     rng = np.random.default_rng(12)
     q, k, v = (rng.standard_normal((1, 2, 256, 64)).astype(np.float32) for _ in range(3))
     shift = rng.standard_normal((1, 2, 1, 64)).astype(np.float32) * 4
-    o1 = orc.sageattn(q.astype(np.float16), k.astype(np.float16), v.astype(np.float16), "fp16", "HND", False, smooth_k=True)
+    o1 = orc.sageattn(q.astype(np.float16), k.astype(np.float16), v.astype(np.float16), "fp16", "HND", False,
+                      smooth_k=True, path="int8")
     o2 = orc.sageattn(q.astype(np.float16), (k + shift).astype(np.float16), v.astype(np.float16), "fp16", "HND", False,
-                      smooth_k=True)
+                      smooth_k=True, path="int8")
     assert cos_sim(o1, o2) > 0.9999
+
+
+# ------------------------------------------------------------------ direct (unquantised) path
+def _textbook_attention_f64(q, k, v_hnd, dtype, layout, sm_scale, causal):
+    """Independent fp64 softmax(sm_scale * Q K^T) V with natural exp, GQA by repeat, plus the fp64
+    log-sum-exp (scipy); q, k in ``layout``/``dtype``, v_hnd the HND values of V as the kernel reads
+    them (fp16).  No fp16 rounding of P anywhere."""
+    from scipy.special import logsumexp
+
+    qh, kh = (orc.to_f32(orc.to_hnd(t, layout), dtype).astype(np.float64) for t in (q, k))
+    G = qh.shape[1] // kh.shape[1]
+    kh, vh = np.repeat(kh, G, axis=1), np.repeat(v_hnd.astype(np.float64), G, axis=1)
+    s = (qh @ kh.transpose(0, 1, 3, 2)) * sm_scale
+    if causal:
+        Sq, Sk = qh.shape[2], kh.shape[2]
+        s = np.where(np.arange(Sk)[None, :] <= np.arange(Sq)[:, None], s, -np.inf)
+    lse = logsumexp(s, axis=-1)
+    return np.exp(s - lse[..., None]) @ vh, lse
+
+
+DIRECT_CASES = [
+    # B, Hq, Hkv, Sq, Sk, D, dtype, layout, causal, sm_scale
+    (1, 4, 2, 150, 150, 64, "fp16", "HND", True, None),
+    (2, 2, 2, 70, 130, 128, "bf16", "NHD", False, None),
+    (1, 3, 1, 90, 40, 128, "fp16", "HND", True, 0.3),
+    (1, 2, 2, 33, 33, 64, "bf16", "HND", False, -0.125),
+]
+
+
+@pytest.mark.parametrize("case", DIRECT_CASES, ids=lambda c: f"{c[6]}_{c[7]}_c{int(c[8])}_sq{c[3]}_sk{c[4]}")
+def test_direct_matches_textbook_fp64_softmax(case):
+    """The direct restatement against an independent fp64 softmax attention: only the fp32 rounding
+    of the scores and the fp16 rounding of P (relative 2^-11 per weight) separate them; a dropped
+    log2 e, a wrong mask, a transposed operand or a wrong GQA head map would not fit."""
+    B, Hq, Hkv, Sq, Sk, D, dtype, layout, causal, sm = case
+    sm_scale = D ** -0.5 if sm is None else sm
+    rng = np.random.default_rng(21)
+
+    def mk(H, S):
+        x = rng.standard_normal((B, H, S, D)).astype(np.float32)
+        x = x if layout == "HND" else np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+        return x.astype(np.float16) if dtype == "fp16" else orc.f32_to_bf16(x)
+
+    q, k, v = mk(Hq, Sq), mk(Hkv, Sk), mk(Hkv, Sk)
+    vt = orc.v_layout(v, dtype, layout)
+    o, lse = orc.attn_direct(q, k, vt, dtype, layout, sm_scale, causal, lse=True)
+    o = orc.to_f32(o, dtype).astype(np.float64)
+    v_vals = orc.to_f32(vt[..., :Sk], "fp16").transpose(0, 1, 3, 2)  # V as fp16, as the kernel reads it
+    ref, ref_lse = _textbook_attention_f64(q, k, v_vals, dtype, layout, sm_scale, causal)
+    tol = 4e-3 if dtype == "bf16" else 2e-3  # output rounding (bf16 has 8 bits) + P rounding
+    assert max_abs(o, ref) < tol
+    assert cos_sim(o, ref) > 0.99999
+    assert np.max(np.abs(lse - ref_lse) / np.maximum(1.0, np.abs(ref_lse))) < 2e-6
+
+
+def test_direct_closed_forms():
+    # zero Q: uniform weights over the live keys -> mean of V's rows; lse = ln(#live)
+    B, H, S, D = 1, 1, 24, 64
+    q = np.zeros((B, H, S, D), np.float16)
+    rng = np.random.default_rng(22)
+    k = rng.standard_normal((B, H, S, D)).astype(np.float16)
+    v = (rng.integers(-4, 5, (B, H, S, D)) * 0.25).astype(np.float16)
+    vt = orc.v_layout(v, "fp16", "HND")
+    o, lse = orc.attn_direct(q, k, vt, "fp16", "HND", 0.125, True, lse=True)
+    want = np.cumsum(v[0, 0].astype(np.float64), axis=0) / np.arange(1, S + 1)[:, None]
+    assert np.max(np.abs(o[0, 0].astype(np.float64) - want)) <= 2.0 ** -10 * np.abs(want).max() + 1e-7
+    assert np.allclose(lse[0, 0], np.log(np.arange(1, S + 1)), rtol=0, atol=1e-12)
+    # one key: output == v exactly, lse == the natural-log score
+    q1 = np.full((1, 1, 1, 64), 0.5, np.float16)
+    k1 = np.full((1, 1, 1, 64), -0.25, np.float16)
+    v1 = rng.standard_normal((1, 1, 1, 64)).astype(np.float16)
+    o1, l1 = orc.attn_direct(q1, k1, orc.v_layout(v1, "fp16", "HND"), "fp16", "HND", 0.125, False, lse=True)
+    assert np.array_equal(o1, v1)
+    s = np.float32(np.float32(-8.0) * orc.sm_scale_log2e(0.125))
+    assert l1[0, 0, 0] == float(s) * math.log(2.0)
+
+
+def test_direct_dispatch_known_answers(monkeypatch):
+    """sageattention/core.py:113-139: the thresholds at their edges, and the env overrides."""
+    for k in [k for k in list(__import__("os").environ) if k.startswith("SAGEATTN_DIRECT_THRESHOLD")]:
+        monkeypatch.delenv(k)
+    u = orc.use_direct_path
+    assert u(64, 2048, 2048, False, "HND") and not u(64, 2049, 2049, False, "HND")
+    assert u(64, 3072, 3072, False, "NHD") and not u(64, 3073, 3073, False, "NHD")
+    assert u(64, 6144, 6144, True, "HND") and not u(64, 6145, 6145, True, "NHD")
+    assert u(64, 100, 6144, False, "HND") and not u(64, 100, 6145, False, "HND")
+    assert u(128, 2048, 2048, True, "HND") and not u(128, 2049, 2049, False, "NHD")
+    assert u(128, 2047, 4096, False, "HND") and not u(128, 2048, 4096, False, "HND")
+    assert not u(128, 100, 4097, True, "HND")
+    monkeypatch.setenv("SAGEATTN_DIRECT_THRESHOLD_D128", "-1")
+    assert not u(128, 1, 1, False, "HND")
+    monkeypatch.setenv("SAGEATTN_DIRECT_THRESHOLD_D64_CAUSAL", "10000")
+    assert u(64, 9000, 9000, True, "HND")
+
+
+def test_product_dispatch_matches_oracle(monkeypatch):
+    """The package's dispatch (host logic, no GPU) agrees with the oracle's restatement."""
+    from sageattention.core import use_direct_path
+
+    for k in [k for k in list(__import__("os").environ) if k.startswith("SAGEATTN_DIRECT_THRESHOLD")]:
+        monkeypatch.delenv(k)
+    for D in (64, 128):
+        for causal in (False, True):
+            for lay in ("HND", "NHD"):
+                for sq in (1, 100, 1024, 2047, 2048, 2049, 3072, 6144, 8192):
+                    for sk in (1, 100, 2048, 2049, 3072, 3073, 4096, 4097, 6144, 6145):
+                        assert use_direct_path(D, sq, sk, causal, lay) == orc.use_direct_path(D, sq, sk, causal, lay)
 
 
 def test_attn_ops_closed_form():
