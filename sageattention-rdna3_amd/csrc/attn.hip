@@ -57,6 +57,15 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kXcds = 8;                   // MI355X: workgroups are dealt round-robin to 8 XCDs
 constexpr float kRescale = 8.0f;           // lazy-rescale threshold of the running max (log2 units)
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (raw dword access)
+// INT8 S accumulators start from the bit pattern of kBias = 1.5 * 2^23 instead
+// of 0: for |acc| < 2^22 (D <= 128 int8 products stay below 2^21) the int32
+// result kBiasBits + acc is the bit pattern of the float kBias + acc, so the
+// softmax reads the scores as floats without an int->float conversion
+constexpr int kBiasBits = 0x4B400000;
+constexpr float kBias = 12582912.0f;
+// tiles whose scales qs*ks stay below this take the conversion-free softmax
+// (its exactness argument needs kBias * sc < 2^23, i.e. sc < 2/3)
+constexpr float kFastScaleLimit = 0.49f;
 
 // Q/K operand kinds
 constexpr int kQkI8 = 0;    // INT8 Q/K (quantized path), per-block scales
@@ -274,11 +283,12 @@ struct OperandMap {
 };
 
 // One QK MFMA: S^T block += K rows (a) . Q^T fragment (b), 32 bytes of each row.
+// The first k-step accumulates onto `init` (INT8: the kBias bit pattern).
 template <int QK>
 __device__ __forceinline__ typename Cfg<64, QK>::SAcc qk_mfma(int4_t a, int4_t b, const typename Cfg<64, QK>::SAcc& c,
-                                                              bool first) {
+                                                              bool first, const typename Cfg<64, QK>::SAcc& init) {
   if constexpr (QK == kQkI8) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, first ? int16_t_{} : c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, first ? init : c, 0, 0, 0);
   } else if constexpr (QK == kQkF16) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b),
                                                   first ? float16_t_{} : c, 0, 0, 0);
@@ -304,12 +314,20 @@ __device__ __forceinline__ typename Cfg<64, QK>::SAcc qk_mfma(int4_t a, int4_t b
 //   pieces 21-36   B(i): e = exp2(y)
 //   pieces 37-52   C(i): fp16 RNE pair into the P^T fragment, partial sums
 //   piece  53      l = l*alpha + sums
-// Scales: INT8 fl(q_scale * k_scale) per 16-key group; direct fl(sm_scale *
+// Scales: INT8 fl(q_scale * k_scale) per 16-key group with its 3 lowest
+// mantissa bits cleared (sc'; relative change < 2^-21); direct fl(sm_scale *
 // log2 e) for all keys.  x -> x*sc is monotonic for sc > 0, so the group max
-// can be taken on the raw accumulators: as int32 for INT8 (dead keys count as
-// INT32_MIN, which no real dot product reaches: |acc| <= 128*128*D < 2^22), as
-// fp32 for the direct path (dead keys -inf).
-template <int D, int QK, bool CAUSAL, bool MASK>
+// can be taken on the raw accumulators: as int32 for INT8 (biased by
+// kBiasBits; dead keys count as INT32_MIN, which no biased dot product
+// reaches), as fp32 for the direct path (dead keys -inf).
+// INT8 scores: the accumulator holds F = kBias + acc as a float, and
+//   y = acc*sc' - m = fma(F, sc', -(kBias*sc' + m))
+// with one rounding.  kBias*sc' is exact (3*sc' fits 24 bits), and so is
+// kBias*sc' + m for an integer reference max m while kBias*sc' < 2^23 and
+// |m| <= kBias*sc' (else the constant rounds by at most |m|*2^-24): FAST uses
+// this form, the other paths fma(float(F - kBias)...) with the same result.
+// The reference max m is kept an integer for INT8 (so alpha is a power of 2).
+template <int D, int QK, bool CAUSAL, bool MASK, bool FAST = false>
 struct TileSoftmax {
   static constexpr int kPieces = 54;
   using SAcc = typename Cfg<D, QK>::SAcc;
@@ -319,6 +337,8 @@ struct TileSoftmax {
   float qs;
   int kt, qrow, hh;
   float sc[4];
+  float bsc[4];   // INT8: kBias * sc (exact)
+  float cg[4];    // INT8 FAST: -(kBias * sc + m_run)
   float gv[4];
   float y[16][2];
   float e[16][2];
@@ -341,8 +361,9 @@ struct TileSoftmax {
   __device__ __forceinline__ void piece(float& m_run, float& l_run, float& alpha, bool& need, half8_t (&pf)[4]) {
     if constexpr (K < 4) {
       constexpr int g = K, nb = g >> 1;
-      sc[g] = QK == kQkI8 ? qs * ks[g] : p.sc;
       if constexpr (QK == kQkI8) {
+        sc[g] = __uint_as_float(__float_as_uint(qs * ks[g]) & ~7u);
+        bsc[g] = kBias * sc[g];
         int gm = INT32_MIN;
 #pragma unroll
         for (int r = (g & 1) * 8; r < (g & 1) * 8 + 8; ++r) {
@@ -350,9 +371,10 @@ struct TileSoftmax {
           if constexpr (MASK) a = dead(nb, r) ? INT32_MIN : a;
           gm = max(gm, a);
         }
-        gv[g] = static_cast<float>(gm) * sc[g];
+        gv[g] = __builtin_fmaf(__int_as_float(gm), sc[g], -bsc[g]);
         if constexpr (MASK) gv[g] = (gm == INT32_MIN) ? -INFINITY : gv[g];
       } else {
+        sc[g] = p.sc;
         float gm = -INFINITY;
 #pragma unroll
         for (int r = (g & 1) * 8; r < (g & 1) * 8 + 8; ++r) {
@@ -372,14 +394,28 @@ struct TileSoftmax {
       const float mx = xhalf_max(__builtin_fmaxf(__builtin_fmaxf(gv[0], gv[1]), __builtin_fmaxf(gv[2], gv[3])));
       need = __builtin_amdgcn_ballot_w64(mx > m_run + kRescale) != 0;
       float m_new = __builtin_fmaxf(m_run, mx);
+      if constexpr (QK == kQkI8) m_new = __builtin_ceilf(m_new);
       m_new = (m_new == -INFINITY) ? 0.0f : m_new;
       m_new = need ? m_new : m_run;
       alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
       m_run = m_new;
+      if constexpr (QK == kQkI8 && FAST) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) cg[g] = -(bsc[g] + m_run);
+      }
     } else if constexpr (K < 21) {
       constexpr int i = K - 5, t = i >> 2, nb = t >> 1, r0 = (t & 1) * 8 + 2 * (i & 3);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) y[i][u] = __builtin_fmaf(static_cast<float>(acc[nb][r0 + u]), sc[t], -m_run);
+      for (int u = 0; u < 2; ++u) {
+        if constexpr (QK == kQkI8 && FAST) {
+          y[i][u] = __builtin_fmaf(__int_as_float(acc[nb][r0 + u]), sc[t], cg[t]);
+        } else if constexpr (QK == kQkI8) {
+          // F - kBias is exact (same binade)
+          y[i][u] = __builtin_fmaf(__int_as_float(acc[nb][r0 + u]) - kBias, sc[t], -m_run);
+        } else {
+          y[i][u] = __builtin_fmaf(acc[nb][r0 + u], sc[t], -m_run);
+        }
+      }
     } else if constexpr (K < 37) {
       constexpr int i = K - 21, t = i >> 2, nb = t >> 1, r0 = (t & 1) * 8 + 2 * (i & 3);
 #pragma unroll
@@ -414,10 +450,12 @@ struct StepMfma {
   const char* vst;
   const char* kst;
   const OperandMap<D, QK>& om;
+  const typename C::SAcc& init;
   int4_t ring[kAhead + 1];
 
-  __device__ __forceinline__ StepMfma(const char* vst_, const char* kst_, const OperandMap<D, QK>& om_)
-      : vst(vst_), kst(kst_), om(om_) {}
+  __device__ __forceinline__ StepMfma(const char* vst_, const char* kst_, const OperandMap<D, QK>& om_,
+                                      const typename C::SAcc& init_)
+      : vst(vst_), kst(kst_), om(om_), init(init_) {}
 
   template <int I>
   __device__ __forceinline__ void read() {
@@ -438,7 +476,7 @@ struct StepMfma {
                                                      0, 0, 0);
     } else {
       constexpr int q = I - kPV, nb = q / C::kDS, ds = q % C::kDS;
-      acc[nb] = qk_mfma<QK>(ring[I % (kAhead + 1)], qf[ds], acc[nb], ds == 0);
+      acc[nb] = qk_mfma<QK>(ring[I % (kAhead + 1)], qf[ds], acc[nb], ds == 0, init);
     }
   }
 };
@@ -522,14 +560,15 @@ __device__ __forceinline__ void step_chunks(std::integer_sequence<int, I...>, St
 // S^T of one 64-key tile for the wave's 32 queries (prologue and masked steps).
 template <int D, int QK>
 __device__ __forceinline__ void qk_tile(const char* kstage, const OperandMap<D, QK>& om,
-                                        const int4_t (&qf)[Cfg<D, QK>::kDS], typename Cfg<D, QK>::SAcc (&acc)[2]) {
+                                        const int4_t (&qf)[Cfg<D, QK>::kDS], typename Cfg<D, QK>::SAcc (&acc)[2],
+                                        const typename Cfg<D, QK>::SAcc& init) {
   using C = Cfg<D, QK>;
 #pragma unroll
   for (int ds = 0; ds < C::kDS; ++ds) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const int4_t a = *reinterpret_cast<const int4_t*>(kstage + nb * 32 * C::kKRow + om.k_off[ds]);
-      acc[nb] = qk_mfma<QK>(a, qf[ds], acc[nb], ds == 0);
+      acc[nb] = qk_mfma<QK>(a, qf[ds], acc[nb], ds == 0, init);
     }
   }
 }
@@ -629,6 +668,23 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) pf[t] = half8_t{};
   float ks[4];
+  // accumulator the first QK k-step starts from (INT8: the kBias bit pattern;
+  // made opaque so that its 16 registers are built once and kept, instead of
+  // being rebuilt from scalars before every first k-step)
+  SAcc sinit;
+  if constexpr (QK == kQkI8) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sinit[r] = kBiasBits;
+    asm volatile("" : "+v"(sinit));
+  } else {
+    sinit = SAcc{};
+  }
+  // INT8: the unmasked loop uses the conversion-free softmax when every k
+  // scale of the block's unmasked tiles is below kFastScaleLimit / qs; the
+  // largest one is found by the block's waves together (each scans an eighth
+  // of the groups, the partial maxima meet in LDS at the prologue barrier).
+  // Otherwise (extreme inputs only) every tile runs in the sequential loop.
+  __shared__ float ks_part[kWaves];
 
   const TileLoader<D, QK> tl(wave, lane, static_cast<int>(p.np), k_pitch);
   // K: rows [0, kv_end) of the head; V_T: the head's padded rows
@@ -658,11 +714,27 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
     tl.issue_k(rk, kring + 0 * C::kKStage, 0, wave);
     tl.issue_k(rk, kring + 1 * C::kKStage, kBN, wave);
     tl.issue_v(make_rsrc(vbase, 0u), vring + 2 * C::kVStage, 0, wave);
-    wait_loads_barrier<0>();
+    if constexpr (QK == kQkI8) {
+      const int ng = n_main * (kBN / SAGE_K_GROUP);
+      const int lo = wave * ng / kWaves, hi = (wave + 1) * ng / kWaves;
+      float mx = 0.0f;
+      for (int g = lo + lane; g < hi; g += 64) mx = __builtin_fmaxf(mx, ksp[g]);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
+      if (lane == 0) ks_part[wave] = mx;
+    }
+    __syncthreads();  // K_0, K_1, V_{-1} landed; ks_part published
+    bool fast_block = true;
+    if constexpr (QK == kQkI8) {
+      float kmax = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) kmax = __builtin_fmaxf(kmax, ks_part[w]);
+      fast_block = qs * kmax < kFastScaleLimit;
+    }
     tl.issue_k(rk, kring + 2 * C::kKStage, 2 * kBN, wave);
     tl.issue_v(rv, vring + 0 * C::kVStage, 0, wave);
     load_ks<QK>(p, ksp, 0, ks);
-    qk_tile<D, QK>(kread, om, qf, s);
+    qk_tile<D, QK>(kread, om, qf, s, sinit);
 
     // Step j (stage index st = j % 3): wait for K_{j+1} and V_{j-1} (issued at
     // step j-2), apply the pending O rescale, issue K_{j+3} into stage j%3 and
@@ -683,17 +755,10 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
       rescale_o();
       tl.issue_k(rk, kring + st * C::kKStage, (j + 3) * kBN, wave);
       tl.issue_v(rv, vring + st1 * C::kVStage, (j + 1) * kBN, wave);
-      if constexpr (!MASKED) {
-        using SM = TileSoftmax<D, QK, CAUSAL, false>;
-        SM sm(p, s, ks, qs, j * kBN, qrow, hh);
-        StepMfma<D, QK> mf(vring + st2 * C::kVStage, kread + st1 * C::kKStage, om);
-        mf.template read<0>();
-        mf.template read<1>();
-        step_chunks<D, QK, SM>(std::make_integer_sequence<int, StepMfma<D, QK>::kN>{}, mf, sm, pf, o, qf, s, m_run,
-                               l_run, alpha, need, pf);
-      } else {
-        // tail / diagonal tiles (a few per block): the same work in plain
-        // order, P.V (reads P) -> softmax (reads S, writes P) -> QK (writes S)
+      // tail / diagonal tiles (a few per block), and INT8 tiles after one with
+      // scales too large for the conversion-free softmax: the same work in
+      // plain order, P.V (reads P) -> softmax (reads S, writes P) -> QK (writes S)
+      auto sequential = [&]() __attribute__((always_inline)) {
         pv_tile<D, QK>(vring + st2 * C::kVStage, om, pf, o);
         auto softmax = [&](auto smask_tag) __attribute__((always_inline)) {
           using SM = TileSoftmax<D, QK, CAUSAL, decltype(smask_tag)::value>;
@@ -707,7 +772,18 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
         } else {
           softmax(std::true_type{});
         }
-        qk_tile<D, QK>(kread + st1 * C::kKStage, om, qf, s);
+        qk_tile<D, QK>(kread + st1 * C::kKStage, om, qf, s, sinit);
+      };
+      if constexpr (!MASKED) {
+        using SM = TileSoftmax<D, QK, CAUSAL, false, true>;
+        SM sm(p, s, ks, qs, j * kBN, qrow, hh);
+        StepMfma<D, QK> mf(vring + st2 * C::kVStage, kread + st1 * C::kKStage, om, sinit);
+        mf.template read<0>();
+        mf.template read<1>();
+        step_chunks<D, QK, SM>(std::make_integer_sequence<int, StepMfma<D, QK>::kN>{}, mf, sm, pf, o, qf, s, m_run,
+                               l_run, alpha, need, pf);
+      } else {
+        sequential();
       }
       // P_j and the row statistics are consumed a step later; pinning them
       // here keeps their computation in this step (otherwise it sinks past
@@ -719,10 +795,12 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
       load_ks<QK>(p, ksp, (j + 1) * kBN, ks);
     };
     int j = 0, st = 0;
-    for (; j + 3 <= n_main; j += 3) {
-      step(j, 0, std::false_type{}, std::integral_constant<int, 0>{});
-      step(j + 1, 1, std::false_type{}, std::integral_constant<int, 1>{});
-      step(j + 2, 2, std::false_type{}, std::integral_constant<int, 2>{});
+    if (fast_block) {
+      for (; j + 3 <= n_main; j += 3) {
+        step(j, 0, std::false_type{}, std::integral_constant<int, 0>{});
+        step(j + 1, 1, std::false_type{}, std::integral_constant<int, 1>{});
+        step(j + 2, 2, std::false_type{}, std::integral_constant<int, 2>{});
+      }
     }
     for (; j < ntiles; ++j) {
       step(j, st, std::true_type{}, std::integral_constant<int, -1>{});

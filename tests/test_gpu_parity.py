@@ -132,6 +132,26 @@ def test_small_shapes_full_parity(cfg):
     _say(f"  worst |gpu-oracle| = {worst:.3g}")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_large_scales_take_the_exact_softmax(causal):
+    """INT8 tiles whose scales q_scale * k_scale reach 0.49 leave the conversion-free softmax for the
+    sequential loop (per wave and block).  Outliers of 300 in one channel of some queries and keys
+    give q_scale * k_scale ~ 0.7 for those waves, while the other waves of the same blocks stay on
+    the fast loop; every row is held to the oracle bar."""
+    cfg = Config("large_scales", 1, 4, 2, 1000, 128, "fp16", "HND", causal, False)
+    _say(f"[large scales] {cfg}")
+    q, k, v = (t.float() for t in make_inputs(cfg, seed=7))
+    k[0, 0, 600:620, 7] = 300.0
+    q[0, 0, 800:840, 7] = 300.0
+    q[0, 1, 100:140, 7] = 300.0
+    q, k, v = (t.to(torch.float16) for t in (q, k, v))
+    pro = gpu_prologue(cfg, q, k, v)
+    assert float(pro["q_scale"].max()) * float(pro["k_scale"].max()) > 0.6
+    o = gpu_attn(cfg, pro, q.dtype)
+    worst = check_rows_vs_oracle(cfg, pro, o, range(cfg.Hq), np.arange(cfg.q_len), cfg.dtype)
+    _say(f"  worst |gpu-oracle| = {worst:.3g}")
+
+
 # ------------------------------------------------------------------ BASELINE sizes
 @pytest.mark.parametrize("cfg", BASELINE_CONFIGS, ids=lambda c: c.name)
 def test_baseline_config_parity(cfg):
