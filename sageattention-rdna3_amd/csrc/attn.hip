@@ -457,6 +457,11 @@ struct StepMfma {
                                       const typename C::SAcc& init_)
       : vst(vst_), kst(kst_), om(om_), init(init_) {}
 
+  // the operand reads of the first kAhead MFMAs
+  template <int... I>
+  __device__ __forceinline__ void read_ahead(std::integer_sequence<int, I...>) {
+    (read<I>(), ...);
+  }
   template <int I>
   __device__ __forceinline__ void read() {
     if constexpr (I < kPV) {
@@ -778,8 +783,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
         using SM = TileSoftmax<D, QK, CAUSAL, false, true>;
         SM sm(p, s, ks, qs, j * kBN, qrow, hh);
         StepMfma<D, QK> mf(vring + st2 * C::kVStage, kread + st1 * C::kKStage, om, sinit);
-        mf.template read<0>();
-        mf.template read<1>();
+        mf.read_ahead(std::make_integer_sequence<int, StepMfma<D, QK>::kAhead>{});
         step_chunks<D, QK, SM>(std::make_integer_sequence<int, StepMfma<D, QK>::kN>{}, mf, sm, pf, o, qf, s, m_run,
                                l_run, alpha, need, pf);
       } else {
