@@ -3,11 +3,11 @@
 
 Workload (BASELINE.json metric): ``sageattn`` at B=1, H=32, S=16384, D=128,
 bf16, HND, causal, smooth_k=False.  A step is one full ``sageattn`` call (V
-layout + INT8 quant of Q/K + fused INT8-QK^T/fp16-PV attention) on inputs
-already resident in HBM; ``value`` is effective TOPS of the whole step:
-4*B*H*D*S(S+1)/2 / step time.
+layout + INT8 quant of K + fused attention that quantises Q itself and runs
+INT8-QK^T / fp16-PV) on inputs already resident in HBM; ``value`` is effective
+TOPS of the whole step: 4*B*H*D*S(S+1)/2 / step time.
 
-``roofline`` is the fused attention kernel alone, timed with HIP events on the
+``roofline`` is that attention kernel alone, timed with HIP events on the
 stream it is launched on (torch's current stream): achieved = the same ops /
 average launch time, against the published dense INT8 MFMA peak of MI355X
 (5.0 POP/s).  ``cpu_baseline`` is the CPU oracle (numpy, all host cores its
@@ -130,11 +130,11 @@ def kernels_only(cfg, q, k, v, n):
     lay = ops.HND if layout == "HND" else ops.NHD
     for _ in range(n):
         mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=q.device, dtype=q.dtype)
-        q8, qs, k8, ks = ops.quant_qk_int8(q, k, mean, lay, D ** -0.5)
+        k8, ks = ops.quant_k_int8(k, mean, lay)
         vt = torch.empty(B, Hkv, D, (S + 63) // 64 * 64, device=q.device, dtype=torch.float16)
         ops.v_transpose(v, vt, lay)
         o = torch.empty_like(q)
-        ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5)
+        ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=q.device)
     dst = torch.empty_like(src)
     for _ in range(n):
@@ -284,7 +284,9 @@ def main():
         return e0.elapsed_time(e1) / n
 
     n_k = max(args.steps, 10)
-    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5), n_k)
+    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n_k)
+    ms_attn_unfused = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5),
+                            n_k)
     # The prologue kernels stream HBM: back to back on the same tensors, part of their traffic would hit the
     # L2 / Infinity Cache (256 MB), so each launch gets its own input set out of NROT (together well past the
     # caches), and the output of a set is written while the next set is read.
@@ -307,6 +309,7 @@ def main():
     qouts = [None] * NROT
     ms_quant = timed(rotated(lambda i: qouts.__setitem__(i, ops.quant_qk_int8(qr[i], kr[i], mean, lay, D ** -0.5))),
                      n_k)
+    ms_kquant = timed(rotated(lambda i: qouts.__setitem__(i, ops.quant_k_int8(kr[i], mean, lay))), n_k)
     ms_vl = timed(rotated(lambda i: ops.v_transpose(vr[i], vtr[i], lay)), n_k)
     ms_mean = timed(rotated(lambda i: ops.mean_seq(kr[i], lay)), n_k) if smooth else 0.0
     del qr, kr, vr, vtr, qouts
@@ -314,11 +317,13 @@ def main():
     achieved = ops_step / (ms_attn * 1e-3) / 1e12
     nq, nk = B * Hq * S * D, B * Hkv * S * D
     quant_bytes = 2 * (nq + nk) + (nq + nk) + 4 * (B * Hq * ((S + 31) // 32) + B * Hkv * ((S + 15) // 16))
+    kquant_bytes = 2 * nk + nk + 4 * B * Hkv * ((S + 15) // 16)
     vl_bytes = 2 * nk + 2 * B * Hkv * D * ((S + 63) // 64 * 64)
     mean_bytes = 2 * nk + 2 * B * Hkv * D
     mixed = 2.0 / (1.0 / PEAK_INT8_TOPS + 1.0 / PEAK_F16_TFLOPS)
     log(f"[bench] attn kernel {ms_attn:.4f} ms = {achieved:.1f} TOPS ({100 * achieved / PEAK_INT8_TOPS:.1f}% INT8 peak); "
-        f"quant {ms_quant * 1e3:.1f} us = {quant_bytes / ms_quant / 1e6:.0f} GB/s; "
+        f"(two-kernel path {ms_attn_unfused:.4f} ms); quant Q+K {ms_quant * 1e3:.1f} us = "
+        f"{quant_bytes / ms_quant / 1e6:.0f} GB/s, K only {ms_kquant * 1e3:.1f} us; "
         f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s")
 
     direct = direct_probe(dev, n_k)
@@ -362,14 +367,17 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_INT8_TOPS, 4),
             "traffic": traffic,
-            "kernel": "attn_fwd_kernel (int8 QK)",
+            "kernel": "attn_fwd_kernel (int8 QK, Q quantised in the kernel)",
             "kernel_ms": round(ms_attn, 5),
+            "two_kernel_path_attn_ms": round(ms_attn_unfused, 5),
             "frac_of_mixed_int8_fp16_ceiling": round(achieved / mixed, 4),
         },
         "prologue": {
             "quant_us": round(ms_quant * 1e3, 2),
             "quant_GBps": round(quant_bytes / ms_quant / 1e6, 1),
             "quant_frac_hbm": round(quant_bytes / ms_quant / 1e6 / PEAK_HBM_GBS, 4),
+            "k_quant_us": round(ms_kquant * 1e3, 2),
+            "k_quant_GBps": round(kquant_bytes / ms_kquant / 1e6, 1),
             "v_layout_us": round(ms_vl * 1e3, 2),
             "v_layout_GBps": round(vl_bytes / ms_vl / 1e6, 1),
             "k_mean_us": round(ms_mean * 1e3, 2) if smooth else None,

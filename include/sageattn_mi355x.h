@@ -135,6 +135,26 @@ int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* val
                          int is_causal, void* stream);
 
 /*
+ * sage_attn_i8_fwd_lse with the Q quantisation done by the attention kernel
+ * itself: `query` is the caller's fp16/bf16 Q (any 16-byte-aligned strides,
+ * HND or NHD, `dtype` = its type and the output's), quantised per 32-token
+ * group exactly as sage_quant_qk_i8 does (scale fl(sm_scale)*log2(e), same
+ * rounding), so the result equals sage_quant_qk_i8 followed by
+ * sage_attn_i8_fwd_lse bit for bit, without the int8 Q round trip through
+ * HBM.  K comes from sage_quant_qk_i8 (called with q_len = 0), V_T from
+ * sage_v_layout; lse may be NULL.
+ * No single reference counterpart: it fuses the Q half of quant_qk_int8
+ * (csrc/attn_gfx11.cu:1974-2067) into qk_int8_sv_bf16_attn_t (:2069-2273).
+ */
+int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* value_t, void* out,
+                            float* lse, const float* k_scale, int dtype,
+                            int64_t batch, int64_t q_heads, int64_t kv_heads,
+                            int64_t q_len, int64_t kv_len, int64_t head_dim,
+                            int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                            int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                            int is_causal, double sm_scale, void* stream);
+
+/*
  * Direct attention without quantisation (the reference's short-sequence
  * branch): S = fp32(q . k) * fl(fl(sm_scale) * log2 e) from fp16/bf16 Q and K
  * (fp32 accumulation), the same masks and online softmax as sage_attn_i8_fwd,

@@ -71,6 +71,8 @@ constexpr float kFastScaleLimit = 0.49f;
 constexpr int kQkI8 = 0;    // INT8 Q/K (quantized path), per-block scales
 constexpr int kQkF16 = 1;   // fp16 Q/K (direct path)
 constexpr int kQkBf16 = 2;  // bf16 Q/K (direct path)
+constexpr int kQkI8F = 3;   // INT8 Q/K, Q quantised by the kernel itself from fp16/bf16
+constexpr bool is_i8(int qk) { return qk == kQkI8 || qk == kQkI8F; }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
@@ -87,6 +89,7 @@ struct AttnParams {
   int64_t o_sb, o_sh, o_sn;
   int64_t np;
   float sc;              // direct path: |fl(sm_scale * log2 e)|
+  float qpre;            // fused Q quantisation: fl(fl(sm_scale) * log2 e)
   uint32_t q_xor;        // direct path: 0x80008000 negates Q (sm_scale < 0), else 0
   int32_t hq, hkv, sq, sk;
   int32_t group;         // Hq / Hkv
@@ -97,7 +100,7 @@ struct AttnParams {
 
 template <int D, int QK>
 struct Cfg {
-  static constexpr int kElem = QK == kQkI8 ? 1 : 2;          // bytes per Q/K element
+  static constexpr int kElem = is_i8(QK) ? 1 : 2;            // bytes per K element in LDS
   static constexpr int kStages = 3;                          // LDS ring depth (K and V)
   static constexpr int kKRow = D * kElem;                    // bytes per K row in LDS (unpadded)
   static constexpr int kVRow = kBN * 2;                      // bytes per V_T row in LDS (unpadded)
@@ -115,7 +118,7 @@ struct Cfg {
   static constexpr int kStepLoads = kVPerWave + (kKLoads >= kWaves ? kKPerWave : 0);
   static constexpr int kDS = kKRow / 32;                     // k-steps of the QK MFMA (32 bytes of a row each)
   static constexpr int kDB = D / 32;                         // 32-row d blocks of O^T
-  using SAcc = std::conditional_t<QK == kQkI8, int16_t_, float16_t_>;  // S^T accumulator block
+  using SAcc = std::conditional_t<is_i8(QK), int16_t_, float16_t_>;  // S^T accumulator block
   static_assert(kVLoads % kWaves == 0, "V tile must split evenly over the waves");
   static_assert(kKLoads < kWaves || kKLoads % kWaves == 0, "K tile must split evenly over the waves");
 };
@@ -250,7 +253,7 @@ __device__ __forceinline__ void wait_loads_barrier() {
 typedef const __attribute__((address_space(4))) float* const_f32_ptr;
 template <int QK>
 __device__ __forceinline__ void load_ks(const AttnParams& p, const float* ksp, int kt, float (&ks)[4]) {
-  if constexpr (QK == kQkI8) {
+  if constexpr (is_i8(QK)) {
     const_f32_ptr kc = (const_f32_ptr)(reinterpret_cast<uint64_t>(uniform_ptr(ksp)));
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -287,7 +290,7 @@ struct OperandMap {
 template <int QK>
 __device__ __forceinline__ typename Cfg<64, QK>::SAcc qk_mfma(int4_t a, int4_t b, const typename Cfg<64, QK>::SAcc& c,
                                                               bool first, const typename Cfg<64, QK>::SAcc& init) {
-  if constexpr (QK == kQkI8) {
+  if constexpr (is_i8(QK)) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, first ? init : c, 0, 0, 0);
   } else if constexpr (QK == kQkF16) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b),
@@ -361,7 +364,7 @@ struct TileSoftmax {
   __device__ __forceinline__ void piece(float& m_run, float& l_run, float& alpha, bool& need, half8_t (&pf)[4]) {
     if constexpr (K < 4) {
       constexpr int g = K, nb = g >> 1;
-      if constexpr (QK == kQkI8) {
+      if constexpr (is_i8(QK)) {
         sc[g] = __uint_as_float(__float_as_uint(qs * ks[g]) & ~7u);
         bsc[g] = kBias * sc[g];
         int gm = INT32_MIN;
@@ -394,12 +397,12 @@ struct TileSoftmax {
       const float mx = xhalf_max(__builtin_fmaxf(__builtin_fmaxf(gv[0], gv[1]), __builtin_fmaxf(gv[2], gv[3])));
       need = __builtin_amdgcn_ballot_w64(mx > m_run + kRescale) != 0;
       float m_new = __builtin_fmaxf(m_run, mx);
-      if constexpr (QK == kQkI8) m_new = __builtin_ceilf(m_new);
+      if constexpr (is_i8(QK)) m_new = __builtin_ceilf(m_new);
       m_new = (m_new == -INFINITY) ? 0.0f : m_new;
       m_new = need ? m_new : m_run;
       alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
       m_run = m_new;
-      if constexpr (QK == kQkI8 && FAST) {
+      if constexpr (is_i8(QK) && FAST) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) cg[g] = -(bsc[g] + m_run);
       }
@@ -407,9 +410,9 @@ struct TileSoftmax {
       constexpr int i = K - 5, t = i >> 2, nb = t >> 1, r0 = (t & 1) * 8 + 2 * (i & 3);
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        if constexpr (QK == kQkI8 && FAST) {
+        if constexpr (is_i8(QK) && FAST) {
           y[i][u] = __builtin_fmaf(__int_as_float(acc[nb][r0 + u]), sc[t], cg[t]);
-        } else if constexpr (QK == kQkI8) {
+        } else if constexpr (is_i8(QK)) {
           // F - kBias is exact (same binade)
           y[i][u] = __builtin_fmaf(__int_as_float(acc[nb][r0 + u]) - kBias, sc[t], -m_run);
         } else {
@@ -593,6 +596,83 @@ __device__ __forceinline__ void pv_tile(const char* vstage, const OperandMap<D, 
   }
 }
 
+// Largest value over the 64 lanes, without LDS: DPP butterflies inside each
+// 16-lane row, then the row and half-wave swaps.
+__device__ __forceinline__ float wave_max64(float v) {
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
+  v = __builtin_fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false)));
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return xhalf_max(v);
+}
+
+// Fused Q quantisation, part 1: lane (m, hh) loads the 16 fp16/bf16 elements
+// 32x + 16hh .. of row wrow0 + m for k-step x, exactly the bytes its Q^T
+// fragment will hold; rows past Sq load as zero (they neither raise the absmax
+// nor reach the output).  Issued first, consumed after the K/V ring loads.
+template <int D>
+__device__ __forceinline__ void load_q_raw(const AttnParams& p, int b, int hq, int qrow, int hh,
+                                           uint32_t (&w)[D / 32][8]) {
+  const uint16_t* qp = static_cast<const uint16_t*>(p.q) + static_cast<int64_t>(b) * p.q_sb +
+                       static_cast<int64_t>(hq) * p.q_sh + static_cast<int64_t>(qrow) * p.q_sn + hh * 16;
+#pragma unroll
+  for (int ds = 0; ds < D / 32; ++ds) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (qrow < p.sq) v = *reinterpret_cast<const uint4*>(qp + ds * 32 + h * 8);
+      w[ds][4 * h + 0] = v.x;
+      w[ds][4 * h + 1] = v.y;
+      w[ds][4 * h + 2] = v.z;
+      w[ds][4 * h + 3] = v.w;
+    }
+  }
+}
+
+// Fused Q quantisation, part 2: the wave's 32 query rows are exactly one Q
+// scale group (32 tokens), quantised with the arithmetic of quant_qk_i8_kernel
+// (csrc/attn_gfx11.cu:179-321 of the reference), so q8 and the returned scale
+// equal the quantisation kernel's bit for bit.
+template <int D, bool BF16>
+__device__ __forceinline__ float quant_q_raw(const AttnParams& p, int wrow0, const uint32_t (&w)[D / 32][8],
+                                             int4_t (&qf)[D / 32]) {
+#pragma clang fp contract(off)
+  constexpr int kDS = D / 32;
+  const float pre = p.qpre;
+  // max |fl(x * pre)| = fl(max |x| * |pre|): rounding is monotonic and
+  // symmetric in sign, so the scaled absmax needs one multiply per group;
+  // fmax ignores NaN elements as the quantisation kernel does
+  float xmax = 0.0f;
+#pragma unroll
+  for (int ds = 0; ds < kDS; ++ds) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float2_t f = unpack2<BF16>(w[ds][k]);
+      xmax = __builtin_fmaxf(xmax, __builtin_fmaxf(__builtin_fabsf(f.x), __builtin_fabsf(f.y)));
+    }
+  }
+  xmax = wave_max64(xmax);
+  const float amax = __builtin_fmaxf(kAmaxFloor, xmax * __builtin_fabsf(pre));
+  const float scale = amax / 127.0f;
+  const float inv = 127.0f / amax;
+  const float iscale = inv * pre;
+#pragma unroll
+  for (int ds = 0; ds < kDS; ++ds) {
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float2_t f0 = unpack2<BF16>(w[ds][2 * k]);
+      const float2_t f1 = unpack2<BF16>(w[ds][2 * k + 1]);
+      o[k] = pack_i8x4(round_half_away_i8(f0.x * iscale), round_half_away_i8(f0.y * iscale),
+                       round_half_away_i8(f1.x * iscale), round_half_away_i8(f1.y * iscale));
+    }
+    qf[ds] = int4_t{static_cast<int>(o[0]), static_cast<int>(o[1]), static_cast<int>(o[2]), static_cast<int>(o[3])};
+  }
+  return wrow0 < p.sq ? scale : 0.0f;
+}
+
 template <int D, int QK, bool CAUSAL, bool OUT_BF16>
 __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   using C = Cfg<D, QK>;
@@ -624,7 +704,11 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   // ---- Q^T fragments (lane (m, hh): bytes 32x + 16hh of row qrow for k-step
   // x) and the wave's q scale
   int4_t qf[C::kDS];
-  {
+  float qs = 1.0f;
+  uint32_t qraw[QK == kQkI8F ? C::kDS : 1][8];  // fused kind: Q as loaded, quantised in the prologue
+  if constexpr (QK == kQkI8F) {
+    load_q_raw<D>(p, b, hq, qrow, hh, qraw);
+  } else {
     const char* qp = static_cast<const char*>(p.q) + hh * 16 +
                      (QK == kQkI8 ? (static_cast<int64_t>(bh) * p.sq + qrow) * D
                                   : (static_cast<int64_t>(b) * p.q_sb + static_cast<int64_t>(hq) * p.q_sh +
@@ -638,19 +722,19 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
       }
       // a negative scale goes into Q's sign bits (exact), so the scale the
       // softmax sees is positive and max commutes with it
-      if constexpr (QK != kQkI8) qf[ds] ^= static_cast<int>(p.q_xor);
+      if constexpr (!is_i8(QK)) qf[ds] ^= static_cast<int>(p.q_xor);
     }
+    if constexpr (QK == kQkI8)
+      qs = (wrow0 < p.sq) ? p.q_scale[static_cast<int64_t>(bh) * p.q_groups + wrow0 / 32] : 0.0f;
   }
-  float qs = 1.0f;
-  if constexpr (QK == kQkI8) qs = (wrow0 < p.sq) ? p.q_scale[static_cast<int64_t>(bh) * p.q_groups + wrow0 / 32] : 0.0f;
 
   const int64_t bhk = static_cast<int64_t>(b) * p.hkv + hk;
-  const char* kbase = static_cast<const char*>(p.k) + (QK == kQkI8 ? bhk * p.sk * D
+  const char* kbase = static_cast<const char*>(p.k) + (is_i8(QK) ? bhk * p.sk * D
                                                                     : (static_cast<int64_t>(b) * p.k_sb + hk * p.k_sh) * C::kElem);
   const uint16_t* vbase = p.vt + bhk * D * p.np;
-  const float* ksp = QK == kQkI8 ? p.k_scale + bhk * p.k_groups : nullptr;
+  const float* ksp = is_i8(QK) ? p.k_scale + bhk * p.k_groups : nullptr;
   // INT8 K is the contiguous quant output: its row pitch is a constant
-  const int k_pitch = QK == kQkI8 ? D : static_cast<int>(p.k_sn) * C::kElem;
+  const int k_pitch = is_i8(QK) ? D : static_cast<int>(p.k_sn) * C::kElem;
 
   const int kv_end = CAUSAL ? min(q0 + kBM, p.sk) : p.sk;
   const int ntiles = (kv_end + kBN - 1) / kBN;
@@ -677,7 +761,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   // made opaque so that its 16 registers are built once and kept, instead of
   // being rebuilt from scalars before every first k-step)
   SAcc sinit;
-  if constexpr (QK == kQkI8) {
+  if constexpr (is_i8(QK)) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) sinit[r] = kBiasBits;
     asm volatile("" : "+v"(sinit));
@@ -719,7 +803,9 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
     tl.issue_k(rk, kring + 0 * C::kKStage, 0, wave);
     tl.issue_k(rk, kring + 1 * C::kKStage, kBN, wave);
     tl.issue_v(make_rsrc(vbase, 0u), vring + 2 * C::kVStage, 0, wave);
-    if constexpr (QK == kQkI8) {
+    // fused kind: quantise Q while K_0, K_1 and V_{-1} are in flight
+    if constexpr (QK == kQkI8F) qs = quant_q_raw<D, OUT_BF16>(p, wrow0, qraw, qf);
+    if constexpr (is_i8(QK)) {
       const int ng = n_main * (kBN / SAGE_K_GROUP);
       const int lo = wave * ng / kWaves, hi = (wave + 1) * ng / kWaves;
       float mx = 0.0f;
@@ -730,7 +816,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
     }
     __syncthreads();  // K_0, K_1, V_{-1} landed; ks_part published
     bool fast_block = true;
-    if constexpr (QK == kQkI8) {
+    if constexpr (is_i8(QK)) {
       float kmax = 0.0f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) kmax = __builtin_fmaxf(kmax, ks_part[w]);
@@ -888,15 +974,16 @@ int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* ou
     return set_error(SAGE_ERR_INVALID_ARG, "q_heads (%lld) must be a multiple of kv_heads (%lld)",
                      static_cast<long long>(q_heads), static_cast<long long>(kv_heads));
   if (batch == 0 || q_len == 0) return SAGE_OK;
-  const bool i8 = qk == kQkI8;
-  if (!out || !q || (i8 && !q_scale) || (kv_len > 0 && (!k || !value_t || (i8 && !k_scale))))
+  const bool i8 = is_i8(qk);
+  if (!out || !q || (qk == kQkI8 && !q_scale) || (kv_len > 0 && (!k || !value_t || (i8 && !k_scale))))
     return set_error(SAGE_ERR_INVALID_ARG, "%s: null pointer argument", fn);
-  const int64_t elem = i8 ? 1 : 2;
+  const int64_t q_elem = qk == kQkI8 ? 1 : 2;
+  const int64_t elem = i8 ? 1 : 2;  // K
   if (!aligned(q, 16) || (kv_len > 0 && (!aligned(k, 16) || !aligned(value_t, 16))))
     return set_error(SAGE_ERR_ALIGNMENT, "%s: q/k/value_t must be 16-byte aligned", fn);
   if (q_sb < 0 || q_sh < 0 || q_sn < 0 || k_sb < 0 || k_sh < 0 || k_sn < head_dim)
     return set_error(SAGE_ERR_INVALID_ARG, "%s: q/k strides must be non-negative and K rows must not overlap", fn);
-  if (((q_sb * elem) % 16) || ((q_sh * elem) % 16) || ((q_sn * elem) % 16) || ((k_sb * elem) % 16) ||
+  if (((q_sb * q_elem) % 16) || ((q_sh * q_elem) % 16) || ((q_sn * q_elem) % 16) || ((k_sb * elem) % 16) ||
       ((k_sh * elem) % 16) || ((k_sn * elem) % 16))
     return set_error(SAGE_ERR_ALIGNMENT, "%s: q/k strides must be multiples of 16 bytes", fn);
   if (!aligned(out, 8) || (o_stride_b % 4) || (o_stride_h % 4) || (o_stride_n % 4))
@@ -934,6 +1021,7 @@ int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* ou
   const float sc = static_cast<float>(sm_scale) * 1.4426950408889634f;
   p.sc = std::fabs(sc);
   p.q_xor = std::signbit(sc) ? 0x80008000u : 0u;
+  p.qpre = sc;  // the quantisation kernel's pre-scale of Q (sign included)
   p.hq = static_cast<int32_t>(q_heads);
   p.hkv = static_cast<int32_t>(kv_heads);
   p.sq = static_cast<int32_t>(q_len);
@@ -946,6 +1034,7 @@ int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* ou
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bf16 = out_dtype == SAGE_DTYPE_BF16;
   if (qk == kQkI8) launch_kind<kQkI8>(p, head_dim, is_causal != 0, bf16, st);
+  else if (qk == kQkI8F) launch_kind<kQkI8F>(p, head_dim, is_causal != 0, bf16, st);
   else if (qk == kQkF16) launch_kind<kQkF16>(p, head_dim, is_causal != 0, bf16, st);
   else launch_kind<kQkBf16>(p, head_dim, is_causal != 0, bf16, st);
   return check_launch(fn);
@@ -994,4 +1083,18 @@ extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const vo
                   batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b,
                   k_stride_h, k_stride_n, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, stream,
                   "sage_attn_direct_fwd");
+}
+
+extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* value_t, void* out,
+                                       float* lse, const float* k_scale, int dtype,
+                                       int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                       int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                       int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                       int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                       int is_causal, double sm_scale, void* stream) {
+  clear_error();
+  return attn_fwd(kQkI8F, query, k_i8, value_t, out, lse, nullptr, k_scale, dtype, batch, q_heads, kv_heads, q_len,
+                  kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n, kv_heads * kv_len * head_dim,
+                  kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, stream,
+                  "sage_attn_i8_fwd_qfused");
 }

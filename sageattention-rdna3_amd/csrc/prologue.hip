@@ -19,22 +19,7 @@ namespace {
 constexpr int kWave = 64;
 constexpr int kQGroup = SAGE_Q_GROUP;  // tokens per Q scale
 constexpr int kKGroup = SAGE_K_GROUP;  // tokens per K scale
-constexpr float kAmaxFloor = 1e-7f;    // csrc/attn_gfx11.cu:192
 constexpr float kLog2e = 1.4426950408889634f;
-
-// float_to_int8 of csrc/attn_gfx11.cu:85-92: fp32 add of +-0.5, truncation
-// toward zero (v_cvt_i32_f32 semantics, NaN -> 0), clamp to [-128, 127].
-__device__ __forceinline__ int round_half_away_i8(float t) {
-  const float u = t + ((t >= 0.0f) ? 0.5f : -0.5f);
-  const float c = __builtin_fminf(__builtin_fmaxf(u, -128.0f), 127.0f);
-  const int r = static_cast<int>(c);
-  return (u == u) ? r : 0;
-}
-
-__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
-  return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
-         ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);
-}
 
 __device__ __forceinline__ float wave_max_xor(float v, int width_log2) {
   // butterfly over lanes xor 1..2^(width_log2-1); max is order independent

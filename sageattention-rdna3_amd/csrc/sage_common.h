@@ -59,4 +59,29 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(t, bf16x2_t));
 }
 
+// ---------------------------------------------------------------- INT8 quantisation (bit-exact)
+// csrc/attn_gfx11.cu:192 of the reference: absmax floor of a scale group.
+constexpr float kAmaxFloor = 1e-7f;
+
+// float_to_int8 of csrc/attn_gfx11.cu:85-92: u = fp32 t + (t >= 0 ? 0.5 : -0.5),
+// clamp to [-128, 127], truncate toward zero (NaN -> 0).  Computed here as
+// trunc(t + copysign(0.5, t)) with v_cvt_i32_f32 (saturating, NaN -> 0) and an
+// integer clamp, which gives the same value for every input: the two forms
+// differ in u only for t = -0 (u = -0.5 instead of 0.5, both truncate to 0),
+// and clamping after truncation equals truncating after clamping because the
+// bounds are integers.  The add must not fuse with the caller's multiply,
+// hence contraction off.
+__device__ __forceinline__ int round_half_away_i8(float t) {
+#pragma clang fp contract(off)
+  const float u = t + __builtin_copysignf(0.5f, t);
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(u));  // saturating, NaN -> 0 (the ISA rule)
+  return min(max(r, -128), 127);
+}
+
+__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
+  return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+         ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);
+}
+
 }  // namespace sage

@@ -73,9 +73,11 @@ def traffic(fetch_csv, write_csv, out_json, out_md, command):
         fb = mean(fetch, k, "FETCH_SIZE") * f_scale
         wb = mean(write, k, "WRITE_SIZE") * w_scale
         res["kernels"][k] = {"fetch_bytes": fb, "write_bytes": wb, "bytes": fb + wb}
-    # attn_fwd_kernel<D, QK, CAUSAL, OUT_BF16>: QK 0 is the INT8 kernel
-    attn = [v for k, v in res["kernels"].items() if k.replace(" ", "").startswith(("attn_fwd_kernel<128,0,",
-                                                                                   "attn_fwd_kernel<64,0,"))]
+    # attn_fwd_kernel<D, QK, CAUSAL, OUT_BF16>: QK 3 is the INT8 kernel that quantises Q itself (the
+    # one sageattn runs), QK 0 the INT8 kernel of the two-kernel op path
+    names = {k.replace(" ", ""): v for k, v in res["kernels"].items()}
+    attn = [v for k, v in names.items() if k.startswith(("attn_fwd_kernel<128,3,", "attn_fwd_kernel<64,3,"))]
+    attn += [v for k, v in names.items() if k.startswith(("attn_fwd_kernel<128,0,", "attn_fwd_kernel<64,0,"))]
     if attn:
         res["attn_bytes_per_launch"] = attn[0]["bytes"]
     json.dump(res, open(out_json, "w"), indent=1)

@@ -55,6 +55,10 @@ SIGNATURES = {
     "sage_attn_i8_fwd_lse": (_I, [_P, _P, _P, _P, _P, _P, _P, _I,
                                   _I64, _I64, _I64, _I64, _I64, _I64,
                                   _I64, _I64, _I64, _I, _P]),
+    "sage_attn_i8_fwd_qfused": (_I, [_P, _P, _P, _P, _P, _P, _I,
+                                     _I64, _I64, _I64, _I64, _I64, _I64,
+                                     _I64, _I64, _I64, _I64, _I64, _I64,
+                                     _I, ctypes.c_double, _P]),
     "sage_attn_direct_fwd": (_I, [_P, _P, _P, _P, _P, _I,
                                   _I64, _I64, _I64, _I64, _I64, _I64,
                                   _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,

@@ -144,11 +144,13 @@ def sageattn(
         k_mean = ops.mean_seq(k, layout_code)
     else:
         k_mean = torch.empty(0, device=q.device, dtype=q.dtype)
-    q_int8, q_scale, k_int8, k_scale = ops.quant_qk_int8(q, k, k_mean, layout_code, sm_scale)
+    # K is quantised by its own kernel; Q is quantised inside the attention kernel (the same q_int8
+    # and q_scale as quant_qk_int8 would produce, so the same output, without the int8 Q round trip)
+    k_int8, k_scale = ops.quant_k_int8(k, k_mean, layout_code)
     # return_lse: the reference returns a zero placeholder (core.py:203-211); the fused kernel writes
     # the real log-sum-exp of each row (natural log, scaled scores; -inf for a row without keys)
-    ops.qk_int8_sv_bf16_attn_t(q_int8, k_int8, v_t, o, q_scale, k_scale,
-                               layout_code, int(is_causal), sm_scale, lse=lse)
+    ops.qk_int8_sv_bf16_attn_qfused_t(q, k_int8, v_t, o, k_scale, layout_code, int(is_causal), sm_scale,
+                                      lse=lse)
 
     if input_dtype == torch.float32:
         o = o.to(torch.float32)

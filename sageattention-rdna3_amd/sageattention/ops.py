@@ -89,6 +89,26 @@ def quant_qk_int8(query: torch.Tensor, key: torch.Tensor, key_mean: torch.Tensor
     return [q8, qs, k8, ks]
 
 
+def quant_k_int8(key: torch.Tensor, key_mean: torch.Tensor, tensor_layout: int) -> List[torch.Tensor]:
+    """The K half of :func:`quant_qk_int8` -> [k_int8, k_scale] (this build's split of the reference
+    op, for the fused-Q attention :func:`qk_int8_sv_bf16_attn_qfused_t`)."""
+    (B, Hkv, Sk, D), (ksb, ksh, ksn) = _bhnd(key, tensor_layout)
+    dev = key.device
+    k8 = torch.empty((B, Hkv, Sk, D), dtype=torch.int8, device=dev)
+    ks = torch.empty((B, Hkv, (Sk + 15) // 16), dtype=torch.float32, device=dev)
+    has_mean = key_mean is not None and key_mean.numel() > 0
+    if has_mean:
+        if tuple(key_mean.shape) != (B, Hkv, D) or key_mean.dtype != key.dtype:
+            raise ValueError(f"key_mean must be [{B},{Hkv},{D}] of {key.dtype}")
+        key_mean = key_mean.contiguous()
+    mean_ptr = _ptr(key_mean) if has_mean else ctypes.c_void_p(0)
+    null = ctypes.c_void_p(0)
+    with torch.cuda.device(dev):
+        _capi.call("sage_quant_qk_i8", null, _ptr(key), mean_ptr, null, null, _ptr(k8), _ptr(ks),
+                   _dtype_code(key), B, Hkv, Hkv, 0, Sk, D, 0, 0, 0, ksb, ksh, ksn, 1.0, _stream(key))
+    return [k8, ks]
+
+
 def v_transpose(value: torch.Tensor, value_t: torch.Tensor, tensor_layout: int) -> torch.Tensor:
     """V -> fp16 V_T [B,H,D,ceil64(N)] written into ``value_t`` (reference
     v_transpose, csrc/attn_gfx11.cu:1889-1935)."""
@@ -193,3 +213,39 @@ def bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, out
     P (reference bf16_attn_t, csrc/attn_gfx11.cu:2376-2472)."""
     return _direct_attn_t("bf16_attn_t", torch.bfloat16, query, key, value, output, tensor_layout, is_causal,
                           sm_scale, lse)
+
+
+def qk_int8_sv_bf16_attn_qfused_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                  output: torch.Tensor, k_scale: torch.Tensor, tensor_layout: int,
+                                  is_causal: int, sm_scale: float,
+                                  lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """:func:`quant_qk_int8` (Q half) + :func:`qk_int8_sv_bf16_attn_t` in one kernel: ``query`` is
+    the fp16/bf16 Q in ``tensor_layout``, quantised inside the attention kernel exactly as the quant
+    op would (same q_int8 and q_scale, so the same output bit for bit); ``key``/``k_scale`` come
+    from :func:`quant_k_int8`, ``value`` is the fp16 V_T.  This build's fusion; no single reference
+    op."""
+    (B, Hq, Sq, D), (qsb, qsh, qsn) = _bhnd(query, tensor_layout)
+    if query.stride(-1) != 1 or output.dtype != query.dtype:
+        raise ValueError("query needs a contiguous head_dim axis and the output's dtype")
+    Bk, Hkv, Sk, Dk = key.shape
+    if Bk != B or Dk != D or key.dtype != torch.int8 or not key.is_contiguous():
+        raise ValueError("key must be contiguous int8 [B,Hkv,Sk,D]")
+    NP = (Sk + 63) // 64 * 64
+    if tuple(value.shape) != (B, Hkv, D, NP) or value.dtype != torch.float16 or not value.is_contiguous():
+        raise ValueError(f"value must be contiguous fp16 V_T [{B},{Hkv},{D},{NP}]")
+    if (tuple(k_scale.shape) != (B, Hkv, (Sk + 15) // 16) or k_scale.dtype != torch.float32
+            or not k_scale.is_contiguous()):
+        raise ValueError("k_scale must be contiguous fp32 [B,Hkv,ceil(Sk/16)]")
+    (Bo, Ho, So, Do), (osb, osh, osn) = _bhnd(output, tensor_layout)
+    if (Bo, Ho, So, Do) != (B, Hq, Sq, D) or output.stride(-1) != 1:
+        raise ValueError("output shape does not match the query")
+    lse_ptr = ctypes.c_void_p(0)
+    if lse is not None:
+        if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+            raise ValueError(f"lse must be contiguous fp32 [{B},{Hq},{Sq}]")
+        lse_ptr = _ptr(lse)
+    with torch.cuda.device(query.device):
+        _capi.call("sage_attn_i8_fwd_qfused", _ptr(query), _ptr(key), _ptr(value), _ptr(output), lse_ptr,
+                   _ptr(k_scale), _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, osb, osh, osn,
+                   int(bool(is_causal)), float(sm_scale), _stream(query))
+    return output

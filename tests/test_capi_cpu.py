@@ -182,6 +182,38 @@ def test_direct_zero_work_is_ok(lib):
     assert lib.sage_last_error() == b""
 
 
+def qfused(lib, **kw):
+    a = dict(q=FAKE, k8=FAKE, vt=FAKE, o=FAKE, lse=NULL, ks=FAKE, dtype=1, B=1, Hq=4, Hkv=2, Sq=64, Sk=64, D=128,
+             qsb=4 * 64 * 128, qsh=64 * 128, qsn=128, osb=4 * 64 * 128, osh=64 * 128, osn=128, causal=1,
+             scale=0.125, stream=NULL)
+    a.update(kw)
+    return lib.sage_attn_i8_fwd_qfused(*a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        (dict(dtype=5), _capi.ERR_INVALID_ARG, "dtype"),
+        (dict(D=96), _capi.ERR_UNSUPPORTED, "head_dim"),
+        (dict(ks=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(q=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(q=ODD), _capi.ERR_ALIGNMENT, "aligned"),
+        (dict(qsn=132), _capi.ERR_ALIGNMENT, "16 bytes"),
+        (dict(osh=130), _capi.ERR_ALIGNMENT, "strides"),
+        (dict(lse=ODD), _capi.ERR_ALIGNMENT, "lse"),
+        (dict(Hq=5), _capi.ERR_INVALID_ARG, "multiple"),
+    ],
+)
+def test_qfused_validation(lib, kw, code, msg):
+    assert qfused(lib, **kw) == code
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_qfused_zero_work_is_ok(lib):
+    assert qfused(lib, Sq=0) == _capi.OK
+    assert qfused(lib, B=0, q=NULL) == _capi.OK
+
+
 def test_v_layout_and_mean_validation(lib):
     assert lib.sage_v_layout(FAKE, FAKE, 0, 1, 2, 100, 80, 0, 0, 0, NULL) == _capi.ERR_UNSUPPORTED
     assert lib.sage_v_layout(ODD, FAKE, 0, 1, 2, 100, 64, 0, 6400, 64, NULL) == _capi.ERR_ALIGNMENT

@@ -152,6 +152,67 @@ def test_large_scales_take_the_exact_softmax(causal):
     _say(f"  worst |gpu-oracle| = {worst:.3g}")
 
 
+# ------------------------------------------------------------------ Q quantisation fused into the attention kernel
+def gpu_fused(cfg: Config, q, k, v, with_lse=False):
+    """K quant + V layout + attention with Q quantised inside the kernel (the ``sageattn`` INT8 path)."""
+    from sageattention import ops
+
+    lay = ops.HND if cfg.layout == "HND" else ops.NHD
+    qd, kd, vd = (t.cuda() for t in (q, k, v))
+    mean = ops.mean_seq(kd, lay) if cfg.smooth_k else torch.empty(0, device="cuda", dtype=kd.dtype)
+    k8, ks = ops.quant_k_int8(kd, mean, lay)
+    NP = (cfg.S + 63) // 64 * 64
+    vt = torch.empty(cfg.B, cfg.Hkv, cfg.D, NP, device="cuda", dtype=torch.float16)
+    ops.v_transpose(vd, vt, lay)
+    o = torch.empty_like(qd)
+    lse = torch.empty((cfg.B, cfg.Hq, cfg.q_len), device="cuda", dtype=torch.float32) if with_lse else None
+    ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o, ks, lay, int(cfg.causal), cfg.D ** -0.5, lse=lse)
+    torch.cuda.synchronize()
+    return o, lse, k8, ks
+
+
+@pytest.mark.parametrize("cfg", [c for c in SMALL if c.dtype != "fp32"] + [BASELINE_CONFIGS[1], BASELINE_CONFIGS[3]],
+                         ids=lambda c: c.name)
+def test_qfused_equals_quant_then_attention(cfg):
+    """Q quantised inside the attention kernel gives the quant kernel's q_int8 / q_scale, so the fused
+    path's output and LSE equal quant_qk_int8 + qk_int8_sv_bf16_attn_t bit for bit; the K-only
+    quantisation equals the K half of the full one."""
+    _say(f"[qfused] {cfg}")
+    q, k, v = make_inputs(cfg, seed=9)
+    pro = gpu_prologue(cfg, q, k, v)
+    o_ref, lse_ref = gpu_attn_lse(cfg, pro, q.dtype)
+    o, lse, k8, ks = gpu_fused(cfg, q, k, v, with_lse=True)
+    assert torch.equal(k8, pro["k8"]) and torch.equal(ks, pro["k_scale"])
+    assert torch.equal(o, o_ref), f"max diff {(o.float() - o_ref.float()).abs().max().item()}"
+    assert torch.equal(lse, lse_ref)
+
+
+def test_qfused_large_scales_and_negative_scale():
+    """The fused quantiser on the extreme-scale inputs (exact-softmax fallback) and with a negative
+    sm_scale (negated q_int8, positive scales), against the two-kernel path."""
+    from sageattention import ops
+
+    cfg = Config("qfused_large", 1, 4, 2, 1000, 128, "fp16", "HND", True, False)
+    q, k, v = (t.float() for t in make_inputs(cfg, seed=7))
+    k[0, 0, 600:620, 7] = 300.0
+    q[0, 0, 800:840, 7] = 300.0
+    q, k, v = (t.to(torch.float16) for t in (q, k, v))
+    pro = gpu_prologue(cfg, q, k, v)
+    o_ref = gpu_attn(cfg, pro, q.dtype)
+    o, _, _, _ = gpu_fused(cfg, q, k, v)
+    assert torch.equal(o, o_ref)
+    qd, kd, vd = (t.cuda() for t in (q, k, v))
+    q8, qs, k8, ks = ops.quant_qk_int8(qd, kd, torch.empty(0, device="cuda", dtype=kd.dtype), ops.HND, -0.07)
+    vt = torch.empty(1, 2, 128, 1024, device="cuda", dtype=torch.float16)
+    ops.v_transpose(vd, vt, ops.HND)
+    o1 = torch.empty_like(qd)
+    ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o1, qs, ks, ops.HND, 1, -0.07)
+    o2 = torch.empty_like(qd)
+    ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o2, ks, ops.HND, 1, -0.07)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
 # ------------------------------------------------------------------ BASELINE sizes
 @pytest.mark.parametrize("cfg", BASELINE_CONFIGS, ids=lambda c: c.name)
 def test_baseline_config_parity(cfg):
