@@ -1,7 +1,7 @@
 """Summaries of rocprofv3 output kept under profiles/ (text only).
 
-  python sageattention-rdna3_amd/profile_summary.py stats STATS_CSV OUT_MD TITLE COMMAND
-      kernel-trace statistics -> markdown table of this library's kernels
+  python sageattention-rdna3_amd/profile_summary.py stats KERNEL_TRACE_CSV OUT_MD TITLE COMMAND
+      kernel trace -> markdown table of this library's kernels, one row per kernel and launch size
   python sageattention-rdna3_amd/profile_summary.py traffic FETCH_CSV WRITE_CSV OUT_JSON OUT_MD COMMAND
       two --pmc runs of `bench.py --kernels-only` (FETCH_SIZE, then WRITE_SIZE) -> HBM bytes per
       launch of every path kernel, each counter scaled by what it reads for the 1 GiB device copy
@@ -46,17 +46,27 @@ def per_kernel(path, counter=None):
     return out
 
 
-def stats(csv_path, out_md, title, command):
-    rows = list(csv.DictReader(open(csv_path)))
-    lines = [f"# {title}", "", "Command (repo root on the GPU box):", "", f"    {command}", "",
-             "Calls include bench.py's warmup, timed steps and its per-kernel HIP-event loops.", "",
-             "| kernel | calls | avg (us) | min (us) | max (us) | share |", "|---|---|---|---|---|---|"]
-    for r in rows:
-        k = short_name(r["Name"])
+def stats(trace_csv, out_md, title, command):
+    """Per (kernel, grid) statistics from the kernel trace: one kernel runs at several shapes in one
+    bench.py run (the NS workload and the direct-path probe), and each shape gets its own row."""
+    groups = collections.defaultdict(list)
+    for r in csv.DictReader(open(trace_csv)):
+        k = short_name(r["Kernel_Name"])
         if k is None or k == "copy_1GiB":
             continue
-        lines.append(f"| `{k}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
-                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {r['Percentage']}% |")
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        blocks = grid // max(1, int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"]))
+        groups[(k, blocks)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in groups.values())
+    lines = [f"# {title}", "", "Command (repo root on the GPU box):", "", f"    {command}", "",
+             "Calls include bench.py's warmup, timed steps and its per-kernel HIP-event loops; one row per kernel "
+             "and launch size (workgroups).", "",
+             "| kernel | workgroups | calls | avg (us) | median (us) | min (us) | max (us) | share |",
+             "|---|---|---|---|---|---|---|---|"]
+    for (k, blocks), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        med = sorted(d)[len(d) // 2]
+        lines.append(f"| `{k}` | {blocks} | {len(d)} | {sum(d) / len(d):.1f} | {med:.1f} | {min(d):.1f} | "
+                     f"{max(d):.1f} | {100 * sum(d) / total:.2f}% |")
     open(out_md, "w").write("\n".join(lines) + "\n")
 
 
