@@ -207,6 +207,64 @@ def direct_probe(dev, n):
     }
 
 
+# the reference's own benchmark shapes (benchmark_attn/benchmark_attn-result-native.txt, all non-causal
+# HND self-attention): name, B, H, S, D, dtype
+REFERENCE_SHAPES = [
+    ("SDXL01", 1, 10, 4096, 64, "fp16"), ("SDXL07", 1, 10, 6144, 64, "fp16"), ("SDXL13", 1, 10, 9216, 64, "fp16"),
+    ("SDXLVAE01", 1, 4, 16384, 128, "fp16"), ("SDXLVAE02", 1, 4, 24576, 128, "fp16"),
+    ("Anima01", 1, 16, 4096, 128, "bf16"), ("AnimaVAE01", 1, 3, 16384, 128, "bf16"),
+    ("Anima03", 1, 16, 6144, 128, "bf16"), ("AnimaVAE02", 1, 3, 24576, 128, "bf16"),
+    ("Anima05", 1, 16, 9216, 128, "bf16"),
+]
+
+
+def reference_shapes_probe(dev, n):
+    """Whole ``sageattn`` calls (quantisation, V layout, attention) at the reference's benchmark shapes,
+    with the library's key-split plan and with splitting switched off (SAGEATTN_KV_SPLITS=1)."""
+    import torch
+
+    from sageattention import _capi, sageattn
+
+    out = []
+    saved = os.environ.get("SAGEATTN_KV_SPLITS")
+    try:
+        for name, B, H, S, D, dt in REFERENCE_SHAPES:
+            cfg = (B, H, H, S, D, dt, "HND", False, False)
+            q, k, v = make_inputs(cfg, dev)
+            res = {}
+            for mode in ("auto", "1"):
+                if mode == "auto":
+                    os.environ.pop("SAGEATTN_KV_SPLITS", None)
+                else:
+                    os.environ["SAGEATTN_KV_SPLITS"] = mode
+                for _ in range(3):
+                    sageattn(q, k, v, tensor_layout="HND", is_causal=False)
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(n):
+                    sageattn(q, k, v, tensor_layout="HND", is_causal=False)
+                e1.record()
+                e1.synchronize()
+                res[mode] = e0.elapsed_time(e1) / n
+            whole, splits = _capi.split_plan(True, B, H, S, S, D, False, 0)
+            flops = attn_ops(B, H, S, S, D, False)
+            out.append({"shape": name, "B": B, "H": H, "S": S, "D": D, "dtype": dt,
+                        "plan": {"whole_qblocks": whole, "splits": splits},
+                        "ms": round(res["auto"], 4), "tops": round(flops / (res["auto"] * 1e-3) / 1e12, 1),
+                        "ms_unsplit": round(res["1"], 4)})
+            log(f"[bench] {name}: sageattn {res['auto']:.4f} ms ({out[-1]['tops']} TOPS), unsplit "
+                f"{res['1']:.4f} ms, plan {whole} whole + splits of {splits}")
+            del q, k, v
+    finally:
+        if saved is None:
+            os.environ.pop("SAGEATTN_KV_SPLITS", None)
+        else:
+            os.environ["SAGEATTN_KV_SPLITS"] = saved
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -327,6 +385,7 @@ def main():
         f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s")
 
     direct = direct_probe(dev, n_k)
+    ref_shapes = reference_shapes_probe(dev, n_k)
 
     traffic = None
     tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")
@@ -384,6 +443,7 @@ def main():
             "k_mean_GBps": round(mean_bytes / ms_mean / 1e6, 1) if smooth else None,
         },
         "direct": direct,
+        "reference_shapes": ref_shapes,
         "device": {"name": props.name, "cus": props.multi_processor_count},
         "cpu_baseline": cpu,
     }

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 1
+#define SAGE_ABI_VERSION 2
 
 /* element types of the fp inputs / outputs */
 #define SAGE_DTYPE_F16 0
@@ -46,6 +46,8 @@ extern "C" {
 #define SAGE_K_GROUP 16
 /* V_T token padding, sageattention/core.py:174. */
 #define SAGE_VT_ALIGN 64
+/* Largest key-split count of the non-causal attention entry points. */
+#define SAGE_MAX_KV_SPLITS 16
 
 /* ABI version of the loaded library (== SAGE_ABI_VERSION it was built with).
  * No reference counterpart (the reference binds through the torch dispatcher). */
@@ -135,14 +137,54 @@ int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* val
                          int is_causal, void* stream);
 
 /*
+ * Key splits of the two entry points below (non-causal launches only).  A
+ * launch has B*Hq*ceil(q_len/256) blocks; when that leaves compute units idle
+ * (fewer blocks than CUs, or a last round partly filled) the key range of
+ * some or all blocks can be split into parts whose fp32 partial outputs and
+ * log-sum-exps a second launch merges exactly
+ * (o = sum_s e^{lse_s - lse} o_s, lse = ln sum_s e^{lse_s}); the result
+ * differs from the unsplit one only by rounding.
+ *   num_splits 0: the library chooses (a cost model over the device's CU
+ *                 count), using only counts whose workspace fits in
+ *                 workspace_bytes (workspace NULL: unsplit);
+ *   num_splits 1: unsplit;
+ *   num_splits n in [2, SAGE_MAX_KV_SPLITS]: n splits (at most one per 64
+ *                 keys); the workspace must hold sage_attn_workspace_bytes().
+ * Causal launches ignore num_splits.  The workspace (16-byte aligned, no
+ * initialisation) is overwritten by the call and may be reused once the call
+ * has completed on its stream; calls sharing one workspace on different
+ * streams race.
+ * Returns the bytes the given launch needs (0: it runs unsplit), or a
+ * negative status.  `quantized` selects sage_attn_i8_fwd_qfused (1) or
+ * sage_attn_direct_fwd (0); with num_splits 0 the answer depends on the
+ * current device.
+ * No reference counterpart (the reference launches one block per q-tile).
+ */
+int64_t sage_attn_workspace_bytes(int quantized, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len,
+                                  int64_t head_dim, int is_causal, int num_splits);
+
+/*
+ * The split plan such a launch runs: q-blocks (256 query rows of one head,
+ * numbered head-major) [0, *whole_qblocks) run whole, and every later one in
+ * *splits key ranges (*splits == 1: nothing is split).  num_splits 0 may
+ * choose to split only the q-blocks of the last, partly filled round of the
+ * device; a forced n > 1 splits every q-block.  Same arguments and
+ * device dependence as sage_attn_workspace_bytes.
+ * No reference counterpart.
+ */
+int sage_attn_split_plan(int quantized, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len,
+                         int64_t head_dim, int is_causal, int num_splits, int64_t* whole_qblocks, int* splits);
+
+/*
  * sage_attn_i8_fwd_lse with the Q quantisation done by the attention kernel
  * itself: `query` is the caller's fp16/bf16 Q (any 16-byte-aligned strides,
  * HND or NHD, `dtype` = its type and the output's), quantised per 32-token
  * group exactly as sage_quant_qk_i8 does (scale fl(sm_scale)*log2(e), same
- * rounding), so the result equals sage_quant_qk_i8 followed by
+ * rounding), so the unsplit result equals sage_quant_qk_i8 followed by
  * sage_attn_i8_fwd_lse bit for bit, without the int8 Q round trip through
  * HBM.  K comes from sage_quant_qk_i8 (called with q_len = 0), V_T from
- * sage_v_layout; lse may be NULL.
+ * sage_v_layout; lse may be NULL.  num_splits / workspace: see
+ * sage_attn_workspace_bytes.
  * No single reference counterpart: it fuses the Q half of quant_qk_int8
  * (csrc/attn_gfx11.cu:1974-2067) into qk_int8_sv_bf16_attn_t (:2069-2273).
  */
@@ -152,7 +194,8 @@ int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* v
                             int64_t q_len, int64_t kv_len, int64_t head_dim,
                             int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
                             int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
-                            int is_causal, double sm_scale, void* stream);
+                            int is_causal, double sm_scale, int num_splits, void* workspace,
+                            int64_t workspace_bytes, void* stream);
 
 /*
  * Direct attention without quantisation (the reference's short-sequence
@@ -162,7 +205,7 @@ int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* v
  * cast to `dtype` (the type of query, key and out).  query/key are read in
  * place through their strides (HND or NHD; multiples of 8 elements, 16-byte
  * aligned bases, key rows must not overlap); lse as in sage_attn_i8_fwd_lse
- * (NULL = not written).
+ * (NULL = not written); num_splits / workspace: see sage_attn_workspace_bytes.
  * Replaces fp16_attn_t / bf16_attn_t (csrc/pybind_gfx11.cpp:24-31,
  * csrc/attn_gfx11.h:21-39, csrc/attn_gfx11.cu:2275-2472; kernels :1465-1885);
  * their bm_sel tile override has no counterpart (one tile shape on gfx950).
@@ -173,7 +216,8 @@ int sage_attn_direct_fwd(const void* query, const void* key, const void* value_t
                          int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
                          int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
                          int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
-                         int is_causal, double sm_scale, void* stream);
+                         int is_causal, double sm_scale, int num_splits, void* workspace,
+                         int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

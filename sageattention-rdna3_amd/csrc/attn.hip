@@ -41,6 +41,7 @@
 //     diagonal tiles;
 //   * block -> work remap keeps consecutive q-blocks of a head on one XCD
 //     (shared L2 for K/V) and issues the heaviest causal blocks first.
+#include <atomic>
 #include <cmath>
 #include <type_traits>
 #include <utility>
@@ -95,7 +96,11 @@ struct AttnParams {
   int32_t group;         // Hq / Hkv
   int32_t nqb;           // query blocks per head
   int32_t q_groups, k_groups;
-  int32_t work;          // B * Hq * nqb
+  int32_t work;          // work items: nfull + (B * Hq * nqb - nfull) * nsplit
+  int32_t nfull;         // q-blocks [0, nfull) run whole (all of them unless the launch splits)
+  int32_t nsplit;        // key-range splits of each later q-block (non-causal only)
+  float* part;           // split items: [items][kBM][D] fp32 partial outputs, each normalised by its own row sum
+  float* part_lse;       // split items: [items][kBM] natural-log LSE of each partial row
 };
 
 template <int D, int QK>
@@ -679,15 +684,26 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   using SAcc = typename C::SAcc;
   __shared__ __align__(16) char smem[C::kSmem];
 
-  // ---- work decode: XCD-contiguous ranges, heaviest causal blocks first
+  // ---- work decode.  q-block id = bh * nqb + (nqb - 1 - qb) (heaviest causal
+  // blocks first).  Blocks [0, nfull) run q-blocks [0, nfull) whole; the later
+  // blocks run the splits of the remaining q-blocks (item = (id - nfull) *
+  // nsplit + split), dispatched after every whole one.  Within each of the two
+  // ranges (nfull is a multiple of the XCD count) consecutive items, i.e. the
+  // q-blocks of a head and the splits of a q-block, stay on one XCD.
   const int L = blockIdx.x;
-  const int xcd = L % kXcds;
-  const int slot = L / kXcds;
-  const int per = p.work / kXcds;
-  const int rem = p.work % kXcds;
-  const int w_idx = xcd * per + (xcd < rem ? xcd : rem) + slot;
-  const int bh = w_idx / p.nqb;
-  const int qb = p.nqb - 1 - (w_idx - bh * p.nqb);
+  const bool whole = L < p.nfull;
+  const int base = whole ? 0 : p.nfull;
+  const int cnt = whole ? p.nfull : p.work - p.nfull;
+  const int xcd = (L - base) % kXcds;
+  const int slot = (L - base) / kXcds;
+  const int per = cnt / kXcds;
+  const int rem = cnt % kXcds;
+  const int w_idx = xcd * per + (xcd < rem ? xcd : rem) + slot;  // item within the range
+  const int nsplit = whole ? 1 : p.nsplit;
+  const int split = whole ? 0 : w_idx % nsplit;
+  const int wq = whole ? w_idx : p.nfull + w_idx / nsplit;
+  const int bh = wq / p.nqb;
+  const int qb = p.nqb - 1 - (wq - bh * p.nqb);
   const int b = bh / p.hq;
   const int hq = bh - b * p.hq;
   const int hk = hq / p.group;
@@ -736,11 +752,17 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   // INT8 K is the contiguous quant output: its row pitch is a constant
   const int k_pitch = is_i8(QK) ? D : static_cast<int>(p.k_sn) * C::kElem;
 
-  const int kv_end = CAUSAL ? min(q0 + kBM, p.sk) : p.sk;
-  const int ntiles = (kv_end + kBN - 1) / kBN;
-  // tiles [0, n_main) need no mask for any wave of the block (inside the key
-  // range and, causal, left of the block's first row)
-  const int n_main = min(CAUSAL ? min(q0, p.sk) / kBN : p.sk / kBN, ntiles);
+  // key tiles of this item: [t0, t0 + ntiles) (non-causal splits take an
+  // even share of the head's tiles; causal blocks end at their last row)
+  const int head_tiles = (p.sk + kBN - 1) / kBN;
+  const int t0 = CAUSAL ? 0 : split * head_tiles / nsplit;
+  const int t1 = CAUSAL ? 0 : (split + 1) * head_tiles / nsplit;
+  const int kv0 = t0 * kBN;
+  const int kv_end = CAUSAL ? min(q0 + kBM, p.sk) : min(t1 * kBN, p.sk);
+  const int ntiles = CAUSAL ? (kv_end + kBN - 1) / kBN : t1 - t0;
+  // tiles [0, n_main) of the item need no mask for any wave of the block
+  // (inside the key range and, causal, left of the block's first row)
+  const int n_main = CAUSAL ? min(min(q0, p.sk) / kBN, ntiles) : (t1 * kBN <= p.sk ? ntiles : ntiles - 1);
 
   float16_t_ o[C::kDB];
 #pragma unroll
@@ -800,14 +822,14 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   if (ntiles > 0) {
     // ---- prologue: K_0, K_1 and a zero V_{-1} (read by step 0's P.V with
     // P = 0), then K_2 and V_0 (what every step issues: K_{j+3}, V_{j+1})
-    tl.issue_k(rk, kring + 0 * C::kKStage, 0, wave);
-    tl.issue_k(rk, kring + 1 * C::kKStage, kBN, wave);
+    tl.issue_k(rk, kring + 0 * C::kKStage, kv0, wave);
+    tl.issue_k(rk, kring + 1 * C::kKStage, kv0 + kBN, wave);
     tl.issue_v(make_rsrc(vbase, 0u), vring + 2 * C::kVStage, 0, wave);
     // fused kind: quantise Q while K_0, K_1 and V_{-1} are in flight
     if constexpr (QK == kQkI8F) qs = quant_q_raw<D, OUT_BF16>(p, wrow0, qraw, qf);
     if constexpr (is_i8(QK)) {
-      const int ng = n_main * (kBN / SAGE_K_GROUP);
-      const int lo = wave * ng / kWaves, hi = (wave + 1) * ng / kWaves;
+      const int g0 = t0 * (kBN / SAGE_K_GROUP), ng = n_main * (kBN / SAGE_K_GROUP);
+      const int lo = g0 + wave * ng / kWaves, hi = g0 + (wave + 1) * ng / kWaves;
       float mx = 0.0f;
       for (int g = lo + lane; g < hi; g += 64) mx = __builtin_fmaxf(mx, ksp[g]);
 #pragma unroll
@@ -822,9 +844,9 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
       for (int w = 0; w < kWaves; ++w) kmax = __builtin_fmaxf(kmax, ks_part[w]);
       fast_block = qs * kmax < kFastScaleLimit;
     }
-    tl.issue_k(rk, kring + 2 * C::kKStage, 2 * kBN, wave);
-    tl.issue_v(rv, vring + 0 * C::kVStage, 0, wave);
-    load_ks<QK>(p, ksp, 0, ks);
+    tl.issue_k(rk, kring + 2 * C::kKStage, kv0 + 2 * kBN, wave);
+    tl.issue_v(rv, vring + 0 * C::kVStage, kv0, wave);
+    load_ks<QK>(p, ksp, kv0, ks);
     qk_tile<D, QK>(kread, om, qf, s, sinit);
 
     // Step j (stage index st = j % 3): wait for K_{j+1} and V_{j-1} (issued at
@@ -844,8 +866,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
       const int st2 = st == 0 ? 2 : st - 1;
       wait_loads_barrier<C::kStepLoads>();
       rescale_o();
-      tl.issue_k(rk, kring + st * C::kKStage, (j + 3) * kBN, wave);
-      tl.issue_v(rv, vring + st1 * C::kVStage, (j + 1) * kBN, wave);
+      tl.issue_k(rk, kring + st * C::kKStage, kv0 + (j + 3) * kBN, wave);
+      tl.issue_v(rv, vring + st1 * C::kVStage, kv0 + (j + 1) * kBN, wave);
       // tail / diagonal tiles (a few per block), and INT8 tiles after one with
       // scales too large for the conversion-free softmax: the same work in
       // plain order, P.V (reads P) -> softmax (reads S, writes P) -> QK (writes S)
@@ -853,12 +875,12 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
         pv_tile<D, QK>(vring + st2 * C::kVStage, om, pf, o);
         auto softmax = [&](auto smask_tag) __attribute__((always_inline)) {
           using SM = TileSoftmax<D, QK, CAUSAL, decltype(smask_tag)::value>;
-          SM sm(p, s, ks, qs, j * kBN, qrow, hh);
+          SM sm(p, s, ks, qs, kv0 + j * kBN, qrow, hh);
           run_all_pieces(sm, std::make_integer_sequence<int, SM::kPieces>{}, m_run, l_run, alpha, need, pf);
         };
         // this wave's keys of tile j are all live: inside the key range and,
         // causal, left of the wave's first row
-        if (j * kBN + kBN - 1 <= (CAUSAL ? min(wrow0, p.sk - 1) : p.sk - 1)) {
+        if (kv0 + j * kBN + kBN - 1 <= (CAUSAL ? min(wrow0, p.sk - 1) : p.sk - 1)) {
           softmax(std::false_type{});
         } else {
           softmax(std::true_type{});
@@ -867,7 +889,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
       };
       if constexpr (!MASKED) {
         using SM = TileSoftmax<D, QK, CAUSAL, false, true>;
-        SM sm(p, s, ks, qs, j * kBN, qrow, hh);
+        SM sm(p, s, ks, qs, kv0 + j * kBN, qrow, hh);
         StepMfma<D, QK> mf(vring + st2 * C::kVStage, kread + st1 * C::kKStage, om, sinit);
         mf.read_ahead(std::make_integer_sequence<int, StepMfma<D, QK>::kAhead>{});
         step_chunks<D, QK, SM>(std::make_integer_sequence<int, StepMfma<D, QK>::kN>{}, mf, sm, pf, o, qf, s, m_run,
@@ -882,7 +904,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
       // k scales of the next tile: issued here, after the step's last LDS
       // read, because a pending scalar load makes every later LDS wait a full
       // lgkmcnt(0) (scalar loads return out of order)
-      load_ks<QK>(p, ksp, (j + 1) * kBN, ks);
+      load_ks<QK>(p, ksp, kv0 + (j + 1) * kBN, ks);
     };
     int j = 0, st = 0;
     if (fast_block) {
@@ -908,6 +930,26 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   // ln(sum_j e^{s_j}) over the natural-log scores s_j = ln2 * (log2-domain
   // score) = ln2 * (m + log2 l), -inf for a row without a live key
   const float l_tot = xhalf_sum(l_run);
+  if (!CAUSAL && nsplit > 1) {
+    // partial result of a key split: O / l in fp32 and its LSE, merged by attn_merge_kernel
+    if (qrow < p.sq) {
+      const int64_t prow = static_cast<int64_t>(w_idx) * kBM + wave * 32 + m;
+      if (hh == 0)
+        p.part_lse[prow] = (l_tot > 0.0f) ? (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f : -INFINITY;
+      const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+      float* pp = p.part + prow * D;
+#pragma unroll
+      for (int db = 0; db < C::kDB; ++db) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int d = db * 32 + 8 * r4 + 4 * hh;
+          *reinterpret_cast<float4*>(pp + d) = make_float4(o[db][4 * r4 + 0] * inv, o[db][4 * r4 + 1] * inv,
+                                                           o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv);
+        }
+      }
+    }
+    return;
+  }
   if (p.lse != nullptr && qrow < p.sq && hh == 0) {
     p.lse[static_cast<int64_t>(bh) * p.sq + qrow] =
         (l_tot > 0.0f) ? (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f : -INFINITY;
@@ -935,6 +977,69 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   }
 }
 
+// ---- merge of key splits: per query row, the partial outputs o_s (each
+// normalised by its own row sum) and their LSEs lse_s combine exactly as
+//   M = max_s lse_s,  w_s = e^{lse_s - M},  o = sum_s w_s o_s / sum_s w_s,
+//   lse = M + ln sum_s w_s
+// (the softmax over the union of the key ranges).  D/4 lanes per row, one
+// float4 of every partial each, so a row's reads are one contiguous run.
+struct MergeParams {
+  const float* part;
+  const float* part_lse;
+  void* out;
+  float* lse;  // [B,Hq,Sq] or null
+  int64_t o_sb, o_sh, o_sn;
+  int64_t rows;  // (split q-blocks) * kBM
+  int32_t hq, sq, nqb, nfull, nsplit;
+};
+
+template <int D, bool OUT_BF16>
+__global__ __launch_bounds__(256) void attn_merge_kernel(MergeParams p) {
+  constexpr int kLanesPerRow = D / 4;
+  constexpr int kRowsPerBlock = 256 / kLanesPerRow;
+  const int64_t gr = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / kLanesPerRow;
+  if (gr >= p.rows) return;
+  const int c = threadIdx.x % kLanesPerRow;
+  // row r of split q-block id = nfull + gr / kBM (the attention kernel's ids)
+  const int64_t sid = gr / kBM;
+  const int r = static_cast<int>(gr - sid * kBM);
+  const int64_t id = p.nfull + sid;
+  const int64_t bh = id / p.nqb;
+  const int qb = p.nqb - 1 - static_cast<int>(id - bh * p.nqb);
+  const int qrow = qb * kBM + r;
+  if (qrow >= p.sq) return;
+  const int64_t item0 = sid * p.nsplit;  // its first split item
+  const float* lp = p.part_lse + item0 * kBM + r;
+  float mx = -INFINITY;
+  for (int s = 0; s < p.nsplit; ++s) mx = fmaxf(mx, lp[s * kBM]);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float wsum = 0.0f;
+  if (mx > -INFINITY) {
+    const float* op = p.part + (item0 * kBM + r) * D + 4 * c;
+    for (int s = 0; s < p.nsplit; ++s) {
+      const float w = expf(lp[s * kBM] - mx);  // 0 for a split without a live key
+      const float4 v = *reinterpret_cast<const float4*>(op + static_cast<int64_t>(s) * kBM * D);
+      wsum += w;
+      acc.x += w * v.x;
+      acc.y += w * v.y;
+      acc.z += w * v.z;
+      acc.w += w * v.w;
+    }
+  }
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+  const int64_t b = bh / p.hq;
+  const int64_t hq = bh - b * p.hq;
+  uint16_t* dst = static_cast<uint16_t*>(p.out) + b * p.o_sb + hq * p.o_sh + static_cast<int64_t>(qrow) * p.o_sn + 4 * c;
+  uint2 w;
+  if constexpr (OUT_BF16) {
+    w = make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
+  } else {
+    w = make_uint2(pack_f16x2(acc.x * inv, acc.y * inv), pack_f16x2(acc.z * inv, acc.w * inv));
+  }
+  *reinterpret_cast<uint2*>(dst) = w;
+  if (c == 0 && p.lse != nullptr) p.lse[bh * p.sq + qrow] = wsum > 0.0f ? mx + logf(wsum) : -INFINITY;
+}
+
 template <int D, int QK, bool CAUSAL>
 void launch(const AttnParams& p, bool out_bf16, hipStream_t st) {
   const dim3 grid(static_cast<uint32_t>(p.work)), block(kThreads);
@@ -956,13 +1061,147 @@ void launch_kind(const AttnParams& p, int64_t head_dim, bool causal, bool out_bf
   }
 }
 
+template <int D>
+void launch_merge(const MergeParams& mp, bool out_bf16, hipStream_t st) {
+  constexpr int kRowsPerBlock = 256 / (D / 4);
+  const dim3 grid(static_cast<uint32_t>(cdiv(mp.rows, kRowsPerBlock))), block(256);
+  if (out_bf16) {
+    attn_merge_kernel<D, true><<<grid, block, 0, st>>>(mp);
+  } else {
+    attn_merge_kernel<D, false><<<grid, block, 0, st>>>(mp);
+  }
+}
+
+// ---- key splits (non-causal only).  A launch of W = B*Hq*ceil(Sq/256)
+// equal blocks runs in ceil(W / CUs) rounds, the last one partly idle (W = 160
+// or 288 on 256 CUs: 38% or 44% of the CU time lost).  A plan (nfull, n) runs
+// q-blocks [0, nfull) whole (nfull: a number of full rounds) and cuts the key
+// range of each remaining q-block into n parts of ceil(T/n) tiles
+// (T = ceil(Sk/64)), whose fp32 partial outputs a merge launch combines:
+//   * nfull = 0: every q-block split (grids smaller than the device);
+//   * nfull = whole rounds: only the last, partial round split.
+// The host picks the plan of least estimated time, with a model fitted to
+// MI355X measurements of this kernel (non-causal, 5 shapes x up to 6 split
+// counts, within ~10%):
+//   item time = (tiles + kItemTiles) * t_tile * (1 + kBusySlowdown * busy)
+// where busy is the fraction of an XCD's CUs running in that round (the chip
+// is power-limited: a tile step takes ~1.5x longer on a full chip than on a
+// lone CU), and merge = kMergeLaunchUs + partial bytes / kMergeBytesPerUs.
+constexpr int kMaxSplits = SAGE_MAX_KV_SPLITS;
+constexpr int kMinSplitTiles = 4;        // keys per split >= 256 (automatic plans)
+constexpr double kItemTiles = 5.3;       // prologue (Q, first K/V tiles) + epilogue, in tile steps
+constexpr double kBusySlowdown = 0.48;
+constexpr double kMergeLaunchUs = 3.0;
+constexpr double kMergeBytesPerUs = 5.5e6;
+// least estimated gain for a plan: the model predicts last-round splits within
+// ~7% but overrates splitting every q-block of a small grid (measured 1.0-1.2x
+// where it predicts 1.1-1.4x)
+constexpr double kMinGainTail = 0.95;    // t_plan < 0.95 t_whole
+constexpr double kMinGainAll = 0.83;     // t_plan < 0.83 t_whole (a 1.2x estimated speed-up)
+
+struct SplitPlan {
+  int64_t nfull;   // q-blocks run whole
+  int64_t nsplit;  // splits of each of the others (1: none)
+};
+
+// Workspace of a plan: fp32 partial rows [items][256][D], then their LSEs [items][256].
+int64_t split_workspace_bytes(int64_t qblocks, const SplitPlan& sp, int64_t head_dim) {
+  return sp.nsplit > 1 ? (qblocks - sp.nfull) * sp.nsplit * kBM * (head_dim + 1) * 4 : 0;
+}
+
+// Compute units of the current device, read once per device (256, the
+// MI355X count, if the runtime cannot tell).
+int device_cus() {
+  constexpr int kDevs = 64;
+  static std::atomic<int> cache[kDevs];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev < kDevs) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) {
+    (void)hipGetLastError();
+    v = 256;
+  }
+  if (dev < kDevs) cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// Time of one 256x64 tile step on a lone CU (us), fitted on MI355X.
+double tile_us(int64_t head_dim, bool quantized) {
+  if (head_dim == 128) return quantized ? 1.06 : 1.3;
+  return quantized ? 0.81 : 0.94;
+}
+
+// `items` equal items of `tiles` tile steps, dealt round-robin over the XCDs.
+double rounds_us(int64_t items, int64_t tiles, double t_tile, int cus) {
+  if (items <= 0) return 0.0;
+  const int64_t per_xcd = cus / kXcds > 0 ? cus / kXcds : 1;
+  const int64_t on_xcd = cdiv(items, kXcds);  // items of the busiest XCD
+  const int64_t full = on_xcd / per_xcd;
+  const int64_t last = on_xcd - full * per_xcd;
+  const double item = (static_cast<double>(tiles) + kItemTiles) * t_tile;
+  double t = static_cast<double>(full) * item * (1.0 + kBusySlowdown);
+  if (last > 0) t += item * (1.0 + kBusySlowdown * static_cast<double>(last) / static_cast<double>(per_xcd));
+  return t;
+}
+
+double plan_us(int64_t qblocks, int64_t tiles, const SplitPlan& sp, int64_t head_dim, bool quantized, int cus) {
+  const double tt = tile_us(head_dim, quantized);
+  if (sp.nsplit <= 1) return rounds_us(qblocks, tiles, tt, cus);
+  const int64_t pieces = (qblocks - sp.nfull) * sp.nsplit;
+  return rounds_us(sp.nfull, tiles, tt, cus) + rounds_us(pieces, cdiv(tiles, sp.nsplit), tt, cus) +
+         kMergeLaunchUs + static_cast<double>(split_workspace_bytes(qblocks, sp, head_dim)) / kMergeBytesPerUs;
+}
+
+// Plan of a launch: num_splits 0 = the least estimated time among the plans
+// whose workspace fits in ws_bytes; 1 = unsplit; n > 1 = every q-block in n
+// splits (at most one per key tile).  Causal launches and empty key ranges
+// are never split.
+SplitPlan plan_splits(bool quantized, int64_t qblocks, int64_t kv_len, int64_t head_dim, bool causal,
+                      int num_splits, int64_t ws_bytes) {
+  const SplitPlan whole{qblocks, 1};
+  if (causal || kv_len <= 0 || num_splits == 1) return whole;
+  const int64_t tiles = cdiv(kv_len, kBN);
+  if (num_splits > 1) {
+    const int64_t n = num_splits < tiles ? num_splits : tiles;
+    return n > 1 ? SplitPlan{0, n} : whole;
+  }
+  const int cus = device_cus();
+  const int64_t round = (cus / kXcds) * kXcds;  // blocks of one full round, a multiple of the XCD count
+  const int64_t tail_full = round > 0 ? (qblocks / round) * round : 0;
+  SplitPlan best = whole;
+  const double base_t = plan_us(qblocks, tiles, whole, head_dim, quantized, cus);
+  double best_score = 1.0;  // estimated time / bar, relative to the whole launch
+  for (int64_t nfull : {int64_t{0}, tail_full}) {
+    if (nfull >= qblocks) continue;
+    const double bar = nfull > 0 ? kMinGainTail : kMinGainAll;
+    for (int64_t n = 2; n <= kMaxSplits && n * kMinSplitTiles <= tiles; ++n) {
+      const SplitPlan sp{nfull, n};
+      if (split_workspace_bytes(qblocks, sp, head_dim) > ws_bytes) break;
+      const double score = plan_us(qblocks, tiles, sp, head_dim, quantized, cus) / (bar * base_t);
+      if (score < best_score) {
+        best_score = score;
+        best = sp;
+      }
+    }
+    if (tail_full == 0) break;
+  }
+  return best;
+}
+
 // Validation and launch shared by the entry points.  Q/K strides are in
 // elements (INT8: the contiguous [B,H,N,D] of the quant outputs).
 int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* out, float* lse, const float* q_scale,
              const float* k_scale, int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t q_len,
              int64_t kv_len, int64_t head_dim, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
              int64_t k_sn, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n, int is_causal, double sm_scale,
-             void* stream, const char* fn) {
+             int num_splits, void* workspace, int64_t workspace_bytes, void* stream, const char* fn) {
   if (out_dtype != SAGE_DTYPE_F16 && out_dtype != SAGE_DTYPE_BF16)
     return set_error(SAGE_ERR_INVALID_ARG, "%s: %s must be SAGE_DTYPE_F16 or SAGE_DTYPE_BF16, got %d", fn,
                      qk == kQkI8 ? "out_dtype" : "dtype", out_dtype);
@@ -973,6 +1212,9 @@ int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* ou
   if (q_heads % kv_heads != 0)
     return set_error(SAGE_ERR_INVALID_ARG, "q_heads (%lld) must be a multiple of kv_heads (%lld)",
                      static_cast<long long>(q_heads), static_cast<long long>(kv_heads));
+  if (num_splits < 0 || num_splits > kMaxSplits || workspace_bytes < 0)
+    return set_error(SAGE_ERR_INVALID_ARG, "%s: num_splits must be in [0, %d] (got %d), workspace_bytes >= 0", fn,
+                     kMaxSplits, num_splits);
   if (batch == 0 || q_len == 0) return SAGE_OK;
   const bool i8 = is_i8(qk);
   if (!out || !q || (qk == kQkI8 && !q_scale) || (kv_len > 0 && (!k || !value_t || (i8 && !k_scale))))
@@ -991,13 +1233,26 @@ int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* ou
   if (lse != nullptr && !aligned(lse, 4))
     return set_error(SAGE_ERR_ALIGNMENT, "%s: lse must be 4-byte aligned", fn);
   const int64_t nqb = cdiv(q_len, kBM);
-  const int64_t work = batch * q_heads * nqb;
+  const int64_t items1 = batch * q_heads * nqb;
   const int64_t np = cdiv(kv_len, SAGE_VT_ALIGN) * SAGE_VT_ALIGN;
   // per-head K and V_T are addressed through 32-bit buffer offsets (K tiles
   // are fetched up to three tiles past the last one)
-  if (q_len > INT32_MAX - kBM || kv_len > INT32_MAX - kBN || work > INT32_MAX || head_dim * np * 2 > UINT32_MAX ||
-      (kv_len + kBN * 5) * k_sn * elem > UINT32_MAX)
+  if (q_len > INT32_MAX - kBM || kv_len > INT32_MAX - kBN || items1 > INT32_MAX / kMaxSplits ||
+      head_dim * np * 2 > UINT32_MAX || (kv_len + kBN * 5) * k_sn * elem > UINT32_MAX)
     return set_error(SAGE_ERR_UNSUPPORTED, "%s: sizes beyond 32-bit limits", fn);
+  const SplitPlan sp = plan_splits(i8, items1, kv_len, head_dim, is_causal != 0, num_splits,
+                                   workspace != nullptr ? workspace_bytes : 0);
+  const int64_t ws_need = split_workspace_bytes(items1, sp, head_dim);
+  if (sp.nsplit > 1) {
+    if (workspace == nullptr || workspace_bytes < ws_need)
+      return set_error(SAGE_ERR_INVALID_ARG, "%s: %lld key splits need a workspace of %lld bytes (got %lld)", fn,
+                       static_cast<long long>(sp.nsplit), static_cast<long long>(ws_need),
+                       static_cast<long long>(workspace != nullptr ? workspace_bytes : 0));
+    if (!aligned(workspace, 16)) return set_error(SAGE_ERR_ALIGNMENT, "%s: workspace must be 16-byte aligned", fn);
+    if ((items1 - sp.nfull) * kBM / (256 / (head_dim / 4)) > INT32_MAX)
+      return set_error(SAGE_ERR_UNSUPPORTED, "%s: sizes beyond 32-bit limits", fn);
+  }
+  const int64_t work = sp.nfull + (items1 - sp.nfull) * sp.nsplit;
 
   AttnParams p;
   p.q = q;
@@ -1031,13 +1286,53 @@ int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* ou
   p.q_groups = static_cast<int32_t>(cdiv(q_len, SAGE_Q_GROUP));
   p.k_groups = static_cast<int32_t>(cdiv(kv_len, SAGE_K_GROUP));
   p.work = static_cast<int32_t>(work);
+  p.nfull = static_cast<int32_t>(sp.nfull);
+  p.nsplit = static_cast<int32_t>(sp.nsplit);
+  const int64_t pieces = (items1 - sp.nfull) * sp.nsplit;
+  p.part = sp.nsplit > 1 ? static_cast<float*>(workspace) : nullptr;
+  p.part_lse = sp.nsplit > 1 ? static_cast<float*>(workspace) + pieces * kBM * head_dim : nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bf16 = out_dtype == SAGE_DTYPE_BF16;
   if (qk == kQkI8) launch_kind<kQkI8>(p, head_dim, is_causal != 0, bf16, st);
   else if (qk == kQkI8F) launch_kind<kQkI8F>(p, head_dim, is_causal != 0, bf16, st);
   else if (qk == kQkF16) launch_kind<kQkF16>(p, head_dim, is_causal != 0, bf16, st);
   else launch_kind<kQkBf16>(p, head_dim, is_causal != 0, bf16, st);
+  if (sp.nsplit > 1) {
+    MergeParams mp;
+    mp.part = p.part;
+    mp.part_lse = p.part_lse;
+    mp.out = out;
+    mp.lse = lse;
+    mp.o_sb = o_stride_b;
+    mp.o_sh = o_stride_h;
+    mp.o_sn = o_stride_n;
+    mp.rows = (items1 - sp.nfull) * kBM;
+    mp.hq = p.hq;
+    mp.sq = p.sq;
+    mp.nqb = p.nqb;
+    mp.nfull = p.nfull;
+    mp.nsplit = p.nsplit;
+    if (head_dim == 128) launch_merge<128>(mp, bf16, st);
+    else launch_merge<64>(mp, bf16, st);
+  }
   return check_launch(fn);
+}
+
+// The plan a launch of this shape will run and the workspace it needs (0: unsplit).
+int64_t attn_split_plan(bool quantized, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len,
+                        int64_t head_dim, int is_causal, int num_splits, SplitPlan* plan_out) {
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(SAGE_ERR_UNSUPPORTED, "head_dim must be 64 or 128, got %lld", static_cast<long long>(head_dim));
+  if (batch < 0 || q_heads <= 0 || q_len < 0 || kv_len < 0 || num_splits < 0 || num_splits > kMaxSplits)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_attn_workspace_bytes: negative size or num_splits outside [0, %d]",
+                     kMaxSplits);
+  const int64_t items1 = batch * q_heads * cdiv(q_len, kBM);
+  *plan_out = SplitPlan{items1, 1};
+  if (batch == 0 || q_len == 0) return 0;
+  if (items1 > INT32_MAX / kMaxSplits)
+    return set_error(SAGE_ERR_UNSUPPORTED, "sage_attn_workspace_bytes: sizes beyond 32-bit limits");
+  *plan_out = plan_splits(quantized, items1, kv_len, head_dim, is_causal != 0, num_splits, INT64_MAX);
+  return split_workspace_bytes(items1, *plan_out, head_dim);
 }
 
 }  // namespace
@@ -1055,7 +1350,7 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
   return attn_fwd(kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads,
                   q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim, head_dim,
                   kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
-                  is_causal, 0.0, stream, "sage_attn_i8_fwd");
+                  is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd");
 }
 
 extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
@@ -1068,7 +1363,7 @@ extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, cons
   return attn_fwd(kQkI8, q_i8, k_i8, value_t, out, lse, q_scale, k_scale, out_dtype, batch, q_heads, kv_heads,
                   q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim, head_dim,
                   kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
-                  is_causal, 0.0, stream, "sage_attn_i8_fwd_lse");
+                  is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd_lse");
 }
 
 extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const void* value_t, void* out, float* lse,
@@ -1077,12 +1372,13 @@ extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const vo
                                     int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
                                     int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
                                     int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
-                                    int is_causal, double sm_scale, void* stream) {
+                                    int is_causal, double sm_scale, int num_splits, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
   clear_error();
   return attn_fwd(dtype == SAGE_DTYPE_BF16 ? kQkBf16 : kQkF16, query, key, value_t, out, lse, nullptr, nullptr, dtype,
                   batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b,
-                  k_stride_h, k_stride_n, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, stream,
-                  "sage_attn_direct_fwd");
+                  k_stride_h, k_stride_n, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits,
+                  workspace, workspace_bytes, stream, "sage_attn_direct_fwd");
 }
 
 extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* value_t, void* out,
@@ -1091,10 +1387,33 @@ extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, co
                                        int64_t q_len, int64_t kv_len, int64_t head_dim,
                                        int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
                                        int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
-                                       int is_causal, double sm_scale, void* stream) {
+                                       int is_causal, double sm_scale, int num_splits, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
   clear_error();
   return attn_fwd(kQkI8F, query, k_i8, value_t, out, lse, nullptr, k_scale, dtype, batch, q_heads, kv_heads, q_len,
                   kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n, kv_heads * kv_len * head_dim,
-                  kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, stream,
-                  "sage_attn_i8_fwd_qfused");
+                  kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits,
+                  workspace, workspace_bytes, stream, "sage_attn_i8_fwd_qfused");
+}
+
+extern "C" int64_t sage_attn_workspace_bytes(int quantized, int64_t batch, int64_t q_heads, int64_t q_len,
+                                             int64_t kv_len, int64_t head_dim, int is_causal, int num_splits) {
+  clear_error();
+  SplitPlan sp;
+  return attn_split_plan(quantized != 0, batch, q_heads, q_len, kv_len, head_dim, is_causal, num_splits, &sp);
+}
+
+extern "C" int sage_attn_split_plan(int quantized, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len,
+                                    int64_t head_dim, int is_causal, int num_splits, int64_t* whole_qblocks,
+                                    int* splits) {
+  clear_error();
+  if (whole_qblocks == nullptr || splits == nullptr)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_attn_split_plan: null output pointer");
+  SplitPlan sp;
+  const int64_t r =
+      attn_split_plan(quantized != 0, batch, q_heads, q_len, kv_len, head_dim, is_causal, num_splits, &sp);
+  if (r < 0) return static_cast<int>(r);
+  *whole_qblocks = sp.nfull;
+  *splits = static_cast<int>(sp.nsplit);
+  return SAGE_OK;
 }

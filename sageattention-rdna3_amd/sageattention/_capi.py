@@ -16,7 +16,8 @@ import threading
 import torch  # noqa: F401  (loads the HIP runtime first)
 
 LIB_NAME = "libsage_mi355x.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
+MAX_KV_SPLITS = 16
 
 DTYPE_F16 = 0
 DTYPE_BF16 = 1
@@ -58,11 +59,13 @@ SIGNATURES = {
     "sage_attn_i8_fwd_qfused": (_I, [_P, _P, _P, _P, _P, _P, _I,
                                      _I64, _I64, _I64, _I64, _I64, _I64,
                                      _I64, _I64, _I64, _I64, _I64, _I64,
-                                     _I, ctypes.c_double, _P]),
+                                     _I, ctypes.c_double, _I, _P, _I64, _P]),
     "sage_attn_direct_fwd": (_I, [_P, _P, _P, _P, _P, _I,
                                   _I64, _I64, _I64, _I64, _I64, _I64,
                                   _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-                                  _I, ctypes.c_double, _P]),
+                                  _I, ctypes.c_double, _I, _P, _I64, _P]),
+    "sage_attn_workspace_bytes": (_I64, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I]),
+    "sage_attn_split_plan": (_I, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I, _P, _P]),
 }
 
 
@@ -126,3 +129,21 @@ def check(func: str, rc: int) -> None:
 def call(func: str, *args) -> None:
     lib = load()
     check(func, getattr(lib, func)(*args))
+
+
+def split_plan(quantized: bool, batch: int, q_heads: int, q_len: int, kv_len: int, head_dim: int,
+               is_causal: bool, num_splits: int = 0):
+    """(whole q-blocks, splits of the others) that such a launch runs on the current device."""
+    whole, splits = ctypes.c_int64(0), ctypes.c_int(0)
+    call("sage_attn_split_plan", int(quantized), batch, q_heads, q_len, kv_len, head_dim, int(bool(is_causal)),
+         int(num_splits), ctypes.byref(whole), ctypes.byref(splits))
+    return whole.value, splits.value
+
+
+def query(func: str, *args) -> int:
+    """Call a size query (non-negative result, or a negative status raised as SageError)."""
+    lib = load()
+    v = getattr(lib, func)(*args)
+    if v < 0:
+        check(func, int(v))
+    return int(v)

@@ -6,7 +6,9 @@ upstream alias and the direct/INT8 dispatch with its thresholds and
 ``SAGEATTN_DIRECT_THRESHOLD_*`` environment overrides, core.py:113-139);
 ``return_lse`` returns the real log-sum-exp where the reference returns a zero
 placeholder.  The reference's Triton backend and ``SAGEATTN_BACKEND`` switch
-(core.py:8,68-76) do not exist here.
+(core.py:8,68-76) do not exist here.  Non-causal launches whose grid leaves
+compute units idle may split each q-block's key range (``SAGEATTN_KV_SPLITS``:
+unset or 0 = the library's choice, 1 = never split, n = n splits).
 """
 from __future__ import annotations
 
@@ -134,7 +136,8 @@ def sageattn(
         if k_token_stride < D:
             k = k.contiguous()
         direct = ops.bf16_attn_t if input_dtype == torch.bfloat16 else ops.fp16_attn_t
-        direct(q, k, v_t, o, layout_code, int(is_causal), sm_scale, 0, lse=lse)
+        direct(q, k, v_t, o, layout_code, int(is_causal), sm_scale, 0, lse=lse,
+               num_splits=_env_int("SAGEATTN_KV_SPLITS", 0))
         if input_dtype == torch.float32:
             o = o.to(torch.float32)
         return (o, lse) if return_lse else o
@@ -150,7 +153,7 @@ def sageattn(
     # return_lse: the reference returns a zero placeholder (core.py:203-211); the fused kernel writes
     # the real log-sum-exp of each row (natural log, scaled scores; -inf for a row without keys)
     ops.qk_int8_sv_bf16_attn_qfused_t(q, k_int8, v_t, o, k_scale, layout_code, int(is_causal), sm_scale,
-                                      lse=lse)
+                                      lse=lse, num_splits=_env_int("SAGEATTN_KV_SPLITS", 0))
 
     if input_dtype == torch.float32:
         o = o.to(torch.float32)

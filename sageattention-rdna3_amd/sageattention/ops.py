@@ -164,9 +164,23 @@ def qk_int8_sv_bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.
     return output
 
 
+def _split_workspace(quantized: bool, B: int, Hq: int, Sq: int, Sk: int, D: int, is_causal: int,
+                     num_splits: int, device: torch.device):
+    """Workspace for the key-split path of a non-causal launch (None when it runs unsplit).  Called
+    with ``device`` current: the library's split choice depends on its CU count."""
+    if not 0 <= int(num_splits) <= _capi.MAX_KV_SPLITS:
+        raise ValueError(f"num_splits must be in [0, {_capi.MAX_KV_SPLITS}], got {num_splits}")
+    nbytes = _capi.query("sage_attn_workspace_bytes", int(quantized), B, Hq, Sq, Sk, D, int(bool(is_causal)),
+                         int(num_splits))
+    if nbytes == 0:
+        return None, ctypes.c_void_p(0), 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return ws, _ptr(ws), nbytes
+
+
 def _direct_attn_t(op: str, want: torch.dtype, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                    output: torch.Tensor, tensor_layout: int, is_causal: int, sm_scale: float,
-                   lse: Optional[torch.Tensor]) -> torch.Tensor:
+                   lse: Optional[torch.Tensor], num_splits: int = 0) -> torch.Tensor:
     for name, t in (("query", query), ("key", key), ("output", output)):
         if t.dtype != want:
             raise ValueError(f"{op}: {name} must be {want}, got {t.dtype}")
@@ -188,42 +202,47 @@ def _direct_attn_t(op: str, want: torch.dtype, query: torch.Tensor, key: torch.T
             raise ValueError(f"{op}: lse must be contiguous fp32 [{B},{Hq},{Sq}]")
         lse_ptr = _ptr(lse)
     with torch.cuda.device(query.device):
+        ws, ws_ptr, ws_bytes = _split_workspace(False, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
         _capi.call("sage_attn_direct_fwd", _ptr(query), _ptr(key), _ptr(value), _ptr(output), lse_ptr,
                    _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, ksb, ksh, ksn, osb, osh, osn,
-                   int(bool(is_causal)), float(sm_scale), _stream(query))
+                   int(bool(is_causal)), float(sm_scale), int(num_splits), ws_ptr, ws_bytes, _stream(query))
+        del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
     return output
 
 
 def fp16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, output: torch.Tensor,
                 tensor_layout: int, is_causal: int, sm_scale: float, bm_sel: int = 0,
-                lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+                lse: Optional[torch.Tensor] = None, num_splits: int = 0) -> torch.Tensor:
     """Direct attention on fp16 Q/K (no quantisation) and the fp16 V_T of
     :func:`v_transpose` into fp16 ``output`` (reference fp16_attn_t,
     csrc/attn_gfx11.cu:2275-2374).  ``bm_sel`` (the reference's experimental
     tile override) is accepted and ignored: gfx950 uses one tile shape.
-    ``lse`` as in :func:`qk_int8_sv_bf16_attn_t`."""
+    ``lse`` as in :func:`qk_int8_sv_bf16_attn_t`.  ``num_splits`` (this
+    build's): key splits of a non-causal launch, 0 = the library's choice for
+    the device, 1 = unsplit, n = n (the workspace is allocated here)."""
     return _direct_attn_t("fp16_attn_t", torch.float16, query, key, value, output, tensor_layout, is_causal,
-                          sm_scale, lse)
+                          sm_scale, lse, num_splits)
 
 
 def bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, output: torch.Tensor,
                 tensor_layout: int, is_causal: int, sm_scale: float, bm_sel: int = 0,
-                lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+                lse: Optional[torch.Tensor] = None, num_splits: int = 0) -> torch.Tensor:
     """bf16 counterpart of :func:`fp16_attn_t`: bf16 Q/K/output, fp16 V_T and
     P (reference bf16_attn_t, csrc/attn_gfx11.cu:2376-2472)."""
     return _direct_attn_t("bf16_attn_t", torch.bfloat16, query, key, value, output, tensor_layout, is_causal,
-                          sm_scale, lse)
+                          sm_scale, lse, num_splits)
 
 
 def qk_int8_sv_bf16_attn_qfused_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                                   output: torch.Tensor, k_scale: torch.Tensor, tensor_layout: int,
                                   is_causal: int, sm_scale: float,
-                                  lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+                                  lse: Optional[torch.Tensor] = None, num_splits: int = 0) -> torch.Tensor:
     """:func:`quant_qk_int8` (Q half) + :func:`qk_int8_sv_bf16_attn_t` in one kernel: ``query`` is
     the fp16/bf16 Q in ``tensor_layout``, quantised inside the attention kernel exactly as the quant
     op would (same q_int8 and q_scale, so the same output bit for bit); ``key``/``k_scale`` come
-    from :func:`quant_k_int8`, ``value`` is the fp16 V_T.  This build's fusion; no single reference
-    op."""
+    from :func:`quant_k_int8`, ``value`` is the fp16 V_T.  ``num_splits`` as in :func:`fp16_attn_t`
+    (the bit-identity with the two-kernel path holds for unsplit launches).  This build's fusion; no
+    single reference op."""
     (B, Hq, Sq, D), (qsb, qsh, qsn) = _bhnd(query, tensor_layout)
     if query.stride(-1) != 1 or output.dtype != query.dtype:
         raise ValueError("query needs a contiguous head_dim axis and the output's dtype")
@@ -245,7 +264,9 @@ def qk_int8_sv_bf16_attn_qfused_t(query: torch.Tensor, key: torch.Tensor, value:
             raise ValueError(f"lse must be contiguous fp32 [{B},{Hq},{Sq}]")
         lse_ptr = _ptr(lse)
     with torch.cuda.device(query.device):
+        ws, ws_ptr, ws_bytes = _split_workspace(True, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
         _capi.call("sage_attn_i8_fwd_qfused", _ptr(query), _ptr(key), _ptr(value), _ptr(output), lse_ptr,
                    _ptr(k_scale), _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, osb, osh, osn,
-                   int(bool(is_causal)), float(sm_scale), _stream(query))
+                   int(bool(is_causal)), float(sm_scale), int(num_splits), ws_ptr, ws_bytes, _stream(query))
+        del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
     return output

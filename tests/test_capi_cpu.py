@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.sage_abi_version() == _capi.ABI_VERSION == 1
+    assert lib.sage_abi_version() == _capi.ABI_VERSION == 2
 
 
 def test_size_helpers(lib):
@@ -146,7 +146,8 @@ def test_attn_lse_zero_work_is_ok(lib):
 def direct(lib, **kw):
     a = dict(q=FAKE, k=FAKE, vt=FAKE, o=FAKE, lse=NULL, dtype=1, B=1, Hq=4, Hkv=2, Sq=64, Sk=64, D=128,
              qsb=4 * 64 * 128, qsh=64 * 128, qsn=128, ksb=2 * 64 * 128, ksh=64 * 128, ksn=128,
-             osb=4 * 64 * 128, osh=64 * 128, osn=128, causal=1, scale=0.125, stream=NULL)
+             osb=4 * 64 * 128, osh=64 * 128, osn=128, causal=1, scale=0.125, nsplit=0, ws=NULL, wsb=0,
+             stream=NULL)
     a.update(kw)
     return lib.sage_attn_direct_fwd(*a.values())
 
@@ -169,6 +170,13 @@ def direct(lib, **kw):
         (dict(osn=130), _capi.ERR_ALIGNMENT, "strides"),
         (dict(lse=ODD), _capi.ERR_ALIGNMENT, "lse"),
         (dict(Sk=2 ** 24, ksn=2 ** 10), _capi.ERR_UNSUPPORTED, "32-bit"),
+        (dict(nsplit=-1), _capi.ERR_INVALID_ARG, "num_splits"),
+        (dict(nsplit=17), _capi.ERR_INVALID_ARG, "num_splits"),
+        (dict(wsb=-16), _capi.ERR_INVALID_ARG, "workspace_bytes"),
+        # 4 key splits of 4 q-blocks: 16 items x 256 rows x (128 + 1) fp32
+        (dict(causal=0, Sk=1024, nsplit=4), _capi.ERR_INVALID_ARG, "need a workspace of 2113536 bytes (got 0)"),
+        (dict(causal=0, Sk=1024, nsplit=4, ws=FAKE, wsb=2113535), _capi.ERR_INVALID_ARG, "2113536"),
+        (dict(causal=0, Sk=1024, nsplit=4, ws=ODD, wsb=2113536), _capi.ERR_ALIGNMENT, "workspace"),
     ],
 )
 def test_direct_validation(lib, kw, code, msg):
@@ -185,7 +193,7 @@ def test_direct_zero_work_is_ok(lib):
 def qfused(lib, **kw):
     a = dict(q=FAKE, k8=FAKE, vt=FAKE, o=FAKE, lse=NULL, ks=FAKE, dtype=1, B=1, Hq=4, Hkv=2, Sq=64, Sk=64, D=128,
              qsb=4 * 64 * 128, qsh=64 * 128, qsn=128, osb=4 * 64 * 128, osh=64 * 128, osn=128, causal=1,
-             scale=0.125, stream=NULL)
+             scale=0.125, nsplit=0, ws=NULL, wsb=0, stream=NULL)
     a.update(kw)
     return lib.sage_attn_i8_fwd_qfused(*a.values())
 
@@ -202,6 +210,9 @@ def qfused(lib, **kw):
         (dict(osh=130), _capi.ERR_ALIGNMENT, "strides"),
         (dict(lse=ODD), _capi.ERR_ALIGNMENT, "lse"),
         (dict(Hq=5), _capi.ERR_INVALID_ARG, "multiple"),
+        (dict(nsplit=99), _capi.ERR_INVALID_ARG, "num_splits"),
+        (dict(causal=0, Sk=4096, Sq=300, nsplit=3), _capi.ERR_INVALID_ARG,
+         f"need a workspace of {2 * 4 * 3 * 256 * 129 * 4} bytes"),
     ],
 )
 def test_qfused_validation(lib, kw, code, msg):
@@ -212,6 +223,54 @@ def test_qfused_validation(lib, kw, code, msg):
 def test_qfused_zero_work_is_ok(lib):
     assert qfused(lib, Sq=0) == _capi.OK
     assert qfused(lib, B=0, q=NULL) == _capi.OK
+
+
+def test_split_workspace_bytes(lib):
+    ws = lib.sage_attn_workspace_bytes
+    # forced counts: items (B*Hq*ceil(Sq/256)) x splits x 256 rows x (D + 1) fp32
+    assert ws(1, 1, 4, 64, 1024, 128, 0, 4) == 4 * 4 * 256 * 129 * 4
+    assert ws(0, 2, 3, 257, 5000, 64, 0, 16) == 2 * 3 * 2 * 16 * 256 * 65 * 4
+    assert ws(1, 1, 4, 64, 128, 128, 0, 4) == 4 * 2 * 256 * 129 * 4  # at most one split per 64 keys
+    assert ws(1, 1, 4, 64, 1024, 128, 0, 1) == 0
+    assert ws(1, 1, 4, 64, 1024, 128, 1, 4) == 0  # causal: never split
+    assert ws(1, 1, 4, 64, 0, 128, 0, 4) == 0
+    assert ws(1, 0, 4, 64, 1024, 128, 0, 4) == 0
+    # the library's own choice: never for a grid of whole rounds
+    assert ws(1, 8, 64, 16384, 16384, 128, 0, 0) == 0
+    assert ws(1, 1, 4, 64, 1024, 128, 0, 17) == _capi.ERR_INVALID_ARG
+    assert ws(1, 1, 4, 64, 1024, 96, 0, 0) == _capi.ERR_UNSUPPORTED
+    assert ws(1, -1, 4, 64, 1024, 128, 0, 0) == _capi.ERR_INVALID_ARG
+    with pytest.raises(_capi.SageError, match="SAGE_ERR_INVALID_ARG"):
+        _capi.query("sage_attn_workspace_bytes", 1, 1, 4, 64, 1024, 128, 0, -1)
+
+
+def test_split_plan(lib):
+    plan = _capi.split_plan
+    assert plan(True, 1, 4, 64, 1024, 128, False, 4) == (0, 4)      # forced: every q-block
+    assert plan(False, 1, 4, 600, 128, 64, False, 9) == (0, 2)      # at most one split per key tile
+    assert plan(True, 1, 4, 600, 4096, 128, True, 4) == (12, 1)     # causal: whole
+    assert plan(True, 1, 4, 600, 4096, 128, False, 1) == (12, 1)
+    assert plan(True, 1, 4, 600, 0, 128, False, 0) == (12, 1)       # no keys
+    assert plan(True, 0, 4, 600, 4096, 128, False, 0) == (0, 1)
+    with pytest.raises(_capi.SageError, match="null output"):
+        _capi.call("sage_attn_split_plan", 1, 1, 4, 64, 1024, 128, 0, 0, NULL, NULL)
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="automatic plans depend on the device's CU count")
+def test_automatic_plans_for_256_cus(lib):
+    """Without a device the planner assumes MI355X's 256 CUs.  Grids of whole rounds stay whole; small
+    grids split every q-block when that promises 1.2x or more; grids over a whole round split only the
+    last round's q-blocks."""
+    plan = _capi.split_plan
+    assert plan(True, 1, 32, 16384, 16384, 128, False, 0) == (2048, 1)   # 8 whole rounds
+    assert plan(True, 1, 16, 4096, 4096, 128, False, 0) == (256, 1)      # exactly one round
+    assert plan(True, 1, 3, 16384, 16384, 128, False, 0) == (192, 1)     # 192 q-blocks: estimated gain < 1.2x
+    assert plan(True, 1, 10, 9216, 9216, 64, False, 0) == (256, 2)       # 360 = 256 + 104
+    assert plan(True, 1, 3, 24576, 24576, 128, False, 0) == (256, 8)     # 288 = 256 + 32
+    assert plan(False, 1, 10, 2048, 2048, 64, False, 0) == (0, 3)        # 80 q-blocks
+    assert plan(True, 2, 144, 256, 4096, 128, False, 0) == (256, 8)
+    # a workspace-size query agrees with the plan: (q-blocks - whole) * splits * 256 rows * (D + 1) fp32
+    assert lib.sage_attn_workspace_bytes(1, 1, 3, 24576, 24576, 128, 0, 0) == 32 * 8 * 256 * 129 * 4
 
 
 def test_v_layout_and_mean_validation(lib):

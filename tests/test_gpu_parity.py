@@ -154,7 +154,8 @@ def test_large_scales_take_the_exact_softmax(causal):
 
 # ------------------------------------------------------------------ Q quantisation fused into the attention kernel
 def gpu_fused(cfg: Config, q, k, v, with_lse=False):
-    """K quant + V layout + attention with Q quantised inside the kernel (the ``sageattn`` INT8 path)."""
+    """K quant + V layout + attention with Q quantised inside the kernel (the ``sageattn`` INT8 path),
+    unsplit (the bit-identity with the two-kernel path is a property of unsplit launches)."""
     from sageattention import ops
 
     lay = ops.HND if cfg.layout == "HND" else ops.NHD
@@ -166,7 +167,8 @@ def gpu_fused(cfg: Config, q, k, v, with_lse=False):
     ops.v_transpose(vd, vt, lay)
     o = torch.empty_like(qd)
     lse = torch.empty((cfg.B, cfg.Hq, cfg.q_len), device="cuda", dtype=torch.float32) if with_lse else None
-    ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o, ks, lay, int(cfg.causal), cfg.D ** -0.5, lse=lse)
+    ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o, ks, lay, int(cfg.causal), cfg.D ** -0.5, lse=lse,
+                                      num_splits=1)
     torch.cuda.synchronize()
     return o, lse, k8, ks
 
@@ -208,7 +210,7 @@ def test_qfused_large_scales_and_negative_scale():
     o1 = torch.empty_like(qd)
     ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o1, qs, ks, ops.HND, 1, -0.07)
     o2 = torch.empty_like(qd)
-    ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o2, ks, ops.HND, 1, -0.07)
+    ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o2, ks, ops.HND, 1, -0.07, num_splits=1)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
 
