@@ -12,8 +12,12 @@ stream it is launched on (torch's current stream): achieved = the same ops /
 average launch time, against the published dense INT8 MFMA peak of MI355X
 (5.0 POP/s).  ``cpu_baseline`` is the CPU oracle (numpy, all host cores its
 BLAS uses) on one head of the same workload, scaled to effective TOPS.
+``reference_shapes`` times whole ``sageattn`` calls at the reference's own
+benchmark shapes (non-causal SDXL / Anima / VAE lines), with and without the
+key splits the library plans for grids that leave CUs idle.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NS|C2|C3|C4|C5]
+       python bench.py --reference-shapes all|NAME[,NAME...]
 """
 from __future__ import annotations
 
@@ -218,9 +222,10 @@ REFERENCE_SHAPES = [
 ]
 
 
-def reference_shapes_probe(dev, n):
-    """Whole ``sageattn`` calls (quantisation, V layout, attention) at the reference's benchmark shapes,
-    with the library's key-split plan and with splitting switched off (SAGEATTN_KV_SPLITS=1)."""
+def reference_shapes_probe(dev, n, names=None):
+    """Whole ``sageattn`` calls (quantisation, V layout, attention) at the reference's benchmark shapes
+    (``names``: a subset), with the library's key-split plan and with splitting switched off
+    (SAGEATTN_KV_SPLITS=1)."""
     import torch
 
     from sageattention import _capi, sageattn
@@ -229,6 +234,8 @@ def reference_shapes_probe(dev, n):
     saved = os.environ.get("SAGEATTN_KV_SPLITS")
     try:
         for name, B, H, S, D, dt in REFERENCE_SHAPES:
+            if names is not None and name not in names:
+                continue
             cfg = (B, H, H, S, D, dt, "HND", False, False)
             q, k, v = make_inputs(cfg, dev)
             res = {}
@@ -273,6 +280,9 @@ def main():
     ap.add_argument("--config", default="NS", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--reference-shapes", default=None, metavar="NAMES",
+                    help="only time sageattn at these reference benchmark shapes (comma list, or 'all'), "
+                         "print them as one JSON line and exit; for rocprofv3 runs of the split path")
     ap.add_argument("--kernels-only", action="store_true",
                     help="launch each path kernel --steps times plus a 1 GiB device copy (the HBM-counter "
                          "calibration) and exit; for rocprofv3 --pmc runs")
@@ -295,6 +305,14 @@ def main():
     B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
     props = torch.cuda.get_device_properties(dev)
     log(f"[bench] device {props.name} CUs={props.multi_processor_count} config={args.config} {cfg}")
+
+    if args.reference_shapes:
+        names = None if args.reference_shapes == "all" else set(args.reference_shapes.split(","))
+        unknown = (names or set()) - {x[0] for x in REFERENCE_SHAPES}
+        if unknown:
+            sys.exit(f"unknown reference shapes: {sorted(unknown)}")
+        print(json.dumps({"reference_shapes": reference_shapes_probe(dev, max(args.steps, 10), names)}), flush=True)
+        return
 
     q, k, v = make_inputs(cfg, dev)
     torch.cuda.synchronize()
