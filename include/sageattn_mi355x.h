@@ -109,7 +109,8 @@ int sage_v_layout(const void* value, void* value_t, int dtype,
  * to fp16, O = P . V_T (fp32 accumulation), out = O / rowsum cast to out_dtype.
  * Inputs are the outputs of sage_quant_qk_i8 and sage_v_layout; GQA maps query
  * head hq to kv head hq / (q_heads / kv_heads).  `out` is [B,Sq,Hq,D] or
- * [B,Hq,Sq,D] by its strides (multiples of 4 elements, 8-byte aligned base).
+ * [B,Hq,Sq,D] by its strides (multiples of 8 elements, 16-byte aligned base,
+ * as the reference's 16-byte output stores need, csrc/attn_gfx11.cu:766-824).
  * Replaces qk_int8_sv_bf16_attn_t (csrc/pybind_gfx11.cpp:19-23,
  * csrc/attn_gfx11.h:10-19, csrc/attn_gfx11.cu:2069-2273; kernel :409-1243).
  */

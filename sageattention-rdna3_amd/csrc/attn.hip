@@ -678,27 +678,14 @@ __device__ __forceinline__ float quant_q_raw(const AttnParams& p, int wrow0, con
   return wrow0 < p.sq ? scale : 0.0f;
 }
 
+// One work item of a block: q-block id = bh * nqb + (nqb - 1 - qb) (heaviest
+// causal blocks first); whole items run q-block w_idx, split items piece
+// w_idx of the split range (q-block nfull + w_idx / nsplit, key range
+// w_idx % nsplit).
 template <int D, int QK, bool CAUSAL, bool OUT_BF16>
-__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
+__device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float* ks_part, bool whole, int w_idx) {
   using C = Cfg<D, QK>;
   using SAcc = typename C::SAcc;
-  __shared__ __align__(16) char smem[C::kSmem];
-
-  // ---- work decode.  q-block id = bh * nqb + (nqb - 1 - qb) (heaviest causal
-  // blocks first).  Blocks [0, nfull) run q-blocks [0, nfull) whole; the later
-  // blocks run the splits of the remaining q-blocks (item = (id - nfull) *
-  // nsplit + split), dispatched after every whole one.  Within each of the two
-  // ranges (nfull is a multiple of the XCD count) consecutive items, i.e. the
-  // q-blocks of a head and the splits of a q-block, stay on one XCD.
-  const int L = blockIdx.x;
-  const bool whole = L < p.nfull;
-  const int base = whole ? 0 : p.nfull;
-  const int cnt = whole ? p.nfull : p.work - p.nfull;
-  const int xcd = (L - base) % kXcds;
-  const int slot = (L - base) / kXcds;
-  const int per = cnt / kXcds;
-  const int rem = cnt % kXcds;
-  const int w_idx = xcd * per + (xcd < rem ? xcd : rem) + slot;  // item within the range
   const int nsplit = whole ? 1 : p.nsplit;
   const int split = whole ? 0 : w_idx % nsplit;
   const int wq = whole ? w_idx : p.nfull + w_idx / nsplit;
@@ -795,8 +782,6 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
   // largest one is found by the block's waves together (each scans an eighth
   // of the groups, the partial maxima meet in LDS at the prologue barrier).
   // Otherwise (extreme inputs only) every tile runs in the sequential loop.
-  __shared__ float ks_part[kWaves];
-
   const TileLoader<D, QK> tl(wave, lane, static_cast<int>(p.np), k_pitch);
   // K: rows [0, kv_end) of the head; V_T: the head's padded rows
   const auto rk = make_rsrc(kbase, kv_end > 0 ? static_cast<uint32_t>((kv_end - 1) * k_pitch + D * C::kElem) : 0u);
@@ -825,13 +810,21 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
     tl.issue_k(rk, kring + 0 * C::kKStage, kv0, wave);
     tl.issue_k(rk, kring + 1 * C::kKStage, kv0 + kBN, wave);
     tl.issue_v(make_rsrc(vbase, 0u), vring + 2 * C::kVStage, 0, wave);
-    // fused kind: quantise Q while K_0, K_1 and V_{-1} are in flight
+    // the first 128 k scales of this wave's share of the scan (up to 16384
+    // keys a block), loaded before the fused quantisation so that their latency
+    // overlaps it
+    const int g0 = t0 * (kBN / SAGE_K_GROUP), ng = n_main * (kBN / SAGE_K_GROUP);
+    const int lo = g0 + wave * ng / kWaves, hi = g0 + (wave + 1) * ng / kWaves;
+    float ks_a = 0.0f, ks_b = 0.0f;
+    if constexpr (is_i8(QK)) {
+      if (lo + lane < hi) ks_a = ksp[lo + lane];
+      if (lo + lane + 64 < hi) ks_b = ksp[lo + lane + 64];
+    }
+    // fused kind: quantise Q while K_0, K_1, V_{-1} and the k scales are in flight
     if constexpr (QK == kQkI8F) qs = quant_q_raw<D, OUT_BF16>(p, wrow0, qraw, qf);
     if constexpr (is_i8(QK)) {
-      const int g0 = t0 * (kBN / SAGE_K_GROUP), ng = n_main * (kBN / SAGE_K_GROUP);
-      const int lo = g0 + wave * ng / kWaves, hi = g0 + (wave + 1) * ng / kWaves;
-      float mx = 0.0f;
-      for (int g = lo + lane; g < hi; g += 64) mx = __builtin_fmaxf(mx, ksp[g]);
+      float mx = __builtin_fmaxf(ks_a, ks_b);
+      for (int g = lo + lane + 128; g < hi; g += 64) mx = __builtin_fmaxf(mx, ksp[g]);
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
       if (lane == 0) ks_part[wave] = mx;
@@ -954,15 +947,28 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
     p.lse[static_cast<int64_t>(bh) * p.sq + qrow] =
         (l_tot > 0.0f) ? (m_run + __builtin_amdgcn_logf(l_tot)) * 0.6931471805599453f : -INFINITY;
   }
-  if (qrow < p.sq) {
+  // Output rows: lane (m, hh) holds 4 consecutive d of row m per (d block,
+  // r4), so stores straight from registers put 16-byte pieces of 32 rows in
+  // every instruction.  Instead the wave stages its 32 rows (cast, 2D bytes
+  // each, rows padded by 16 bytes so that the 32 rows of one write start in
+  // different banks) in its part of the LDS ring, which is free once every
+  // wave's last P.V has read it, and writes whole rows: each store
+  // instruction then covers 64 lanes x 16 bytes of 4 (D=128) or 8 (D=64)
+  // consecutive rows.
+  {
+    constexpr int kRowB = D * 2;
+    constexpr int kPitch = kRowB + 16;
+    constexpr int kChunks = kRowB / 16;
+    constexpr int kRowsPerStore = 64 / kChunks;
+    static_assert(kWaves * 32 * kPitch <= C::kSmem, "output staging exceeds the LDS ring");
     const float inv = (l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
-    uint16_t* op = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(b) * p.o_sb +
-                   static_cast<int64_t>(qrow) * p.o_sn + static_cast<int64_t>(hq) * p.o_sh;
+    char* const ost = smem + wave * (32 * kPitch);
+    __syncthreads();  // every wave's last P.V has read the ring
+    char* const wbase = ost + m * kPitch + 8 * hh;
 #pragma unroll
     for (int db = 0; db < C::kDB; ++db) {
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = db * 32 + 8 * r4 + 4 * hh;
         const float v0 = o[db][4 * r4 + 0] * inv, v1 = o[db][4 * r4 + 1] * inv;
         const float v2 = o[db][4 * r4 + 2] * inv, v3 = o[db][4 * r4 + 3] * inv;
         uint2 w;
@@ -971,9 +977,104 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
         } else {
           w = make_uint2(pack_f16x2(v0, v1), pack_f16x2(v2, v3));
         }
-        *reinterpret_cast<uint2*>(op + d) = w;
+        // d = 32 db + 8 r4 + 4 hh: byte 64 db + 16 r4 + 8 hh of the row
+        *reinterpret_cast<uint2*>(wbase + 64 * db + 16 * r4) = w;
       }
     }
+    const int lr = lane / kChunks, lc = lane % kChunks;
+    const char* const rbase = ost + lr * kPitch + lc * 16;
+    uint16_t* const obase = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(b) * p.o_sb +
+                            static_cast<int64_t>(hq) * p.o_sh + static_cast<int64_t>(wrow0 + lr) * p.o_sn + lc * 8;
+#pragma unroll
+    for (int i = 0; i < 32 / kRowsPerStore; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(rbase + i * kRowsPerStore * kPitch);
+      if (wrow0 + lr + i * kRowsPerStore < p.sq)
+        *reinterpret_cast<uint4*>(obase + static_cast<int64_t>(i * kRowsPerStore) * p.o_sn) = v;
+    }
+  }
+}
+
+// Grid: one block per item when there are at most as many items as CUs;
+// otherwise a persistent grid of one block per CU (a multiple of the XCD
+// count, block L on XCD L % 8) walks a static schedule.  The hardware
+// dispatcher refills a CU only in order, and with causal blocks of unequal
+// length that left CUs idle for 11 us on average between blocks at
+// B1 H32 S16384 (3 us between equal blocks); the static schedule has no such
+// gaps.  Items are dealt in XCD-contiguous ranges (the q-blocks of a head and
+// the splits of a q-block share an XCD's L2, and the blocks of one round
+// stream the same K/V tiles); within a range the blocks of the XCD take
+// consecutive items in rounds, in snake order for causal items (reversed in
+// odd rounds).  A head's causal q-blocks come heaviest first, so a forward
+// round and the reversed one after it give every block the same number of key
+// tiles whenever a head's q-blocks fill a whole number of round pairs or two
+// rounds cover whole heads (B1 H32 S16384: 64 q-blocks per head, 32 blocks
+// per XCD).  Whole items precede split items.
+// Item k of block L (false past its last).  One item per block (grid ==
+// work): blocks [0, nfull) whole items, then the split items, each range
+// XCD-contiguous (nfull is a multiple of the XCD count).  Persistent grid:
+// range 0 (whole) then range 1 (split); block (xcd, slot) takes, in rounds r,
+// index r * nb + slot of its XCD's share of the range (snake order for causal
+// items: nb - 1 - slot in odd rounds).
+template <bool CAUSAL>
+__device__ __forceinline__ bool next_item(const AttnParams& p, int L, int k, bool& whole, int& w_idx) {
+  if (static_cast<int>(gridDim.x) == p.work) {
+    if (k > 0) return false;
+    whole = L < p.nfull;
+    const int base = whole ? 0 : p.nfull;
+    const int cnt = whole ? p.nfull : p.work - p.nfull;
+    const int xcd = (L - base) % kXcds;
+    const int slot = (L - base) / kXcds;
+    const int per = cnt / kXcds;
+    const int rem = cnt % kXcds;
+    w_idx = xcd * per + (xcd < rem ? xcd : rem) + slot;
+    return true;
+  }
+  const int xcd = L % kXcds;
+  const int slot = L / kXcds;
+  const int nb = static_cast<int>(gridDim.x) / kXcds;  // blocks per XCD
+#pragma unroll
+  for (int range = 0; range < 2; ++range) {
+    whole = range == 0;
+    const int cnt = whole ? p.nfull : p.work - p.nfull;
+    const int per = cnt / kXcds;
+    const int rem = cnt % kXcds;
+    const int first = xcd * per + (xcd < rem ? xcd : rem);
+    const int n_x = per + (xcd < rem ? 1 : 0);
+    // this block's items in the range: the full rounds plus maybe one
+    const int rounds = n_x / nb;
+    const int pos_last = (CAUSAL && (rounds & 1)) ? nb - 1 - slot : slot;
+    const int mine = rounds + (pos_last < n_x - rounds * nb ? 1 : 0);
+    if (k < mine) {
+      w_idx = first + k * nb + ((CAUSAL && (k & 1)) ? nb - 1 - slot : slot);
+      return true;
+    }
+    k -= mine;
+  }
+  return false;
+}
+
+// Grid: one block per item when there are at most as many items as CUs;
+// otherwise a persistent grid of one block per CU (a multiple of the XCD
+// count, block L on XCD L % 8) walks a static schedule.  The hardware
+// dispatcher refills a CU only in order, and with causal blocks of unequal
+// length that left CUs idle for 11 us on average between blocks at
+// B1 H32 S16384 (3 us between equal blocks); the static schedule has no such
+// gaps.  Items are dealt in XCD-contiguous ranges (the q-blocks of a head and
+// the splits of a q-block share an XCD's L2); within a range the blocks of
+// the XCD take items in rounds, causal items heaviest first (over the heads
+// of the range) and in snake order, so every block's total of key tiles is
+// the same whenever the range is whole heads and an even number of rounds.
+// Whole items precede split items.
+template <int D, int QK, bool CAUSAL, bool OUT_BF16>
+__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(AttnParams p) {
+  using C = Cfg<D, QK>;
+  __shared__ __align__(16) char smem[C::kSmem];
+  __shared__ float ks_part[kWaves];
+  bool whole;
+  int w_idx;
+  for (int k = 0; next_item<CAUSAL>(p, blockIdx.x, k, whole, w_idx); ++k) {
+    if (k > 0) __syncthreads();  // the item reuses the LDS ring and ks_part
+    attn_item<D, QK, CAUSAL, OUT_BF16>(p, smem, ks_part, whole, w_idx);
   }
 }
 
@@ -1040,9 +1141,15 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(MergeParams p) {
   if (c == 0 && p.lse != nullptr) p.lse[bh * p.sq + qrow] = wsum > 0.0f ? mx + logf(wsum) : -INFINITY;
 }
 
+int device_cus();
+
 template <int D, int QK, bool CAUSAL>
 void launch(const AttnParams& p, bool out_bf16, hipStream_t st) {
-  const dim3 grid(static_cast<uint32_t>(p.work)), block(kThreads);
+  // persistent grid (one block per CU, a multiple of the XCD count) when the
+  // items outnumber the CUs
+  const int round = (device_cus() / kXcds) * kXcds;
+  const int blocks = (round >= kXcds && p.work > round) ? round : p.work;
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(kThreads);
   if (out_bf16) {
     attn_fwd_kernel<D, QK, CAUSAL, true><<<grid, block, 0, st>>>(p);
   } else {
@@ -1228,8 +1335,9 @@ int attn_fwd(int qk, const void* q, const void* k, const void* value_t, void* ou
   if (((q_sb * q_elem) % 16) || ((q_sh * q_elem) % 16) || ((q_sn * q_elem) % 16) || ((k_sb * elem) % 16) ||
       ((k_sh * elem) % 16) || ((k_sn * elem) % 16))
     return set_error(SAGE_ERR_ALIGNMENT, "%s: q/k strides must be multiples of 16 bytes", fn);
-  if (!aligned(out, 8) || (o_stride_b % 4) || (o_stride_h % 4) || (o_stride_n % 4))
-    return set_error(SAGE_ERR_ALIGNMENT, "%s: out needs an 8-byte aligned base and strides that are multiples of 4", fn);
+  if (!aligned(out, 16) || (o_stride_b % 8) || (o_stride_h % 8) || (o_stride_n % 8))
+    return set_error(SAGE_ERR_ALIGNMENT, "%s: out needs a 16-byte aligned base and strides that are multiples of 8",
+                     fn);
   if (lse != nullptr && !aligned(lse, 4))
     return set_error(SAGE_ERR_ALIGNMENT, "%s: lse must be 4-byte aligned", fn);
   const int64_t nqb = cdiv(q_len, kBM);
