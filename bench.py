@@ -280,6 +280,8 @@ def main():
     ap.add_argument("--config", default="NS", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-probes", action="store_true",
+                    help="skip the direct-kernel and reference-shape probes (kernel traces of the NS workload alone)")
     ap.add_argument("--reference-shapes", default=None, metavar="NAMES",
                     help="only time sageattn at these reference benchmark shapes (comma list, or 'all'), "
                          "print them as one JSON line and exit; for rocprofv3 runs of the split path")
@@ -402,8 +404,8 @@ def main():
         f"{quant_bytes / ms_quant / 1e6:.0f} GB/s, K only {ms_kquant * 1e3:.1f} us; "
         f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s")
 
-    direct = direct_probe(dev, n_k)
-    ref_shapes = reference_shapes_probe(dev, n_k)
+    direct = None if args.no_probes else direct_probe(dev, n_k)
+    ref_shapes = None if args.no_probes else reference_shapes_probe(dev, n_k)
 
     traffic = None
     tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")
