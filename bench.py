@@ -134,9 +134,7 @@ def kernels_only(cfg, q, k, v, n):
     lay = ops.HND if layout == "HND" else ops.NHD
     for _ in range(n):
         mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=q.device, dtype=q.dtype)
-        k8, ks = ops.quant_k_int8(k, mean, lay)
-        vt = torch.empty(B, Hkv, D, (S + 63) // 64 * 64, device=q.device, dtype=torch.float16)
-        ops.v_transpose(v, vt, lay)
+        k8, ks, vt = ops.prep_kv_int8(k, v, mean, lay)
         o = torch.empty_like(q)
         ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5)
     src = torch.empty(1 << 30, dtype=torch.uint8, device=q.device)
@@ -388,6 +386,7 @@ def main():
     ms_quant = timed(rotated(lambda i: qouts.__setitem__(i, ops.quant_qk_int8(qr[i], kr[i], mean, lay, D ** -0.5))),
                      n_k)
     ms_kquant = timed(rotated(lambda i: qouts.__setitem__(i, ops.quant_k_int8(kr[i], mean, lay))), n_k)
+    ms_prep = timed(rotated(lambda i: qouts.__setitem__(i, ops.prep_kv_int8(kr[i], vr[i], mean, lay))), n_k)
     ms_vl = timed(rotated(lambda i: ops.v_transpose(vr[i], vtr[i], lay)), n_k)
     ms_mean = timed(rotated(lambda i: ops.mean_seq(kr[i], lay)), n_k) if smooth else 0.0
     del qr, kr, vr, vtr, qouts
@@ -402,7 +401,8 @@ def main():
     log(f"[bench] attn kernel {ms_attn:.4f} ms = {achieved:.1f} TOPS ({100 * achieved / PEAK_INT8_TOPS:.1f}% INT8 peak); "
         f"(two-kernel path {ms_attn_unfused:.4f} ms); quant Q+K {ms_quant * 1e3:.1f} us = "
         f"{quant_bytes / ms_quant / 1e6:.0f} GB/s, K only {ms_kquant * 1e3:.1f} us; "
-        f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s")
+        f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s; K quant + V layout in one launch "
+        f"{ms_prep * 1e3:.1f} us = {(kquant_bytes + vl_bytes) / ms_prep / 1e6:.0f} GB/s")
 
     direct = None if args.no_probes else direct_probe(dev, n_k)
     ref_shapes = None if args.no_probes else reference_shapes_probe(dev, n_k)
@@ -457,6 +457,9 @@ def main():
             "quant_frac_hbm": round(quant_bytes / ms_quant / 1e6 / PEAK_HBM_GBS, 4),
             "k_quant_us": round(ms_kquant * 1e3, 2),
             "k_quant_GBps": round(kquant_bytes / ms_kquant / 1e6, 1),
+            "prep_kv_us": round(ms_prep * 1e3, 2),
+            "prep_kv_GBps": round((kquant_bytes + vl_bytes) / ms_prep / 1e6, 1),
+            "prep_kv_frac_hbm": round((kquant_bytes + vl_bytes) / ms_prep / 1e6 / PEAK_HBM_GBS, 4),
             "v_layout_us": round(ms_vl * 1e3, 2),
             "v_layout_GBps": round(vl_bytes / ms_vl / 1e6, 1),
             "k_mean_us": round(ms_mean * 1e3, 2) if smooth else None,

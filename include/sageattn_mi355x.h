@@ -104,6 +104,21 @@ int sage_v_layout(const void* value, void* value_t, int dtype,
                   int64_t stride_b, int64_t stride_h, int64_t stride_n, void* stream);
 
 /*
+ * The K half of sage_quant_qk_i8 (K minus key_mean when non-NULL, groups of
+ * SAGE_K_GROUP tokens) and sage_v_layout in one launch, with the same outputs
+ * bit for bit: k_i8 [B,Hkv,Sk,D] int8 and k_scale [B,Hkv,ceil(Sk/16)] fp32
+ * (contiguous), value_t [B,Hkv,D,padded_len] fp16.  key and value share
+ * `dtype`, each with its own strides.  What sageattn runs before
+ * sage_attn_i8_fwd_qfused (which quantises Q itself).
+ * No single reference counterpart: the K half of quant_qk_int8
+ * (csrc/attn_gfx11.cu:1974-2067) plus v_transpose (:1889-1935).
+ */
+int sage_prep_kv_i8(const void* key, const void* value, const void* key_mean, int8_t* k_i8, float* k_scale,
+                    void* value_t, int dtype, int64_t batch, int64_t kv_heads, int64_t kv_len, int64_t head_dim,
+                    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                    int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n, void* stream);
+
+/*
  * Fused attention: S = (q_i8 . k_i8) * q_scale * k_scale (log2 domain), causal
  * mask top-left (key j > query i masked), online softmax with exp2, P rounded
  * to fp16, O = P . V_T (fp32 accumulation), out = O / rowsum cast to out_dtype.

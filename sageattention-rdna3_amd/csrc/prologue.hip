@@ -51,12 +51,10 @@ struct QuantParams {
 // owns 16-byte column chunk `cc` of rows h*16 + rsub + i*RPI (i < ITER), so
 // every load instruction covers whole rows and every store is coalesced.
 template <bool BF16, int D>
-__global__ __launch_bounds__(256) void quant_qk_i8_kernel(QuantParams p) {
+__device__ __forceinline__ void quant_unit(const QuantParams& p, int64_t unit, int lane) {
   constexpr int CPR = D / 8;       // 16-byte chunks per row
   constexpr int RPI = 32 / CPR;    // rows per iteration per half wave
   constexpr int ITER = 16 / RPI;   // iterations per lane
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t unit = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (unit >= p.n_units) return;
   const bool is_q = unit < p.n_q_units;
   const int64_t u = is_q ? unit : unit - p.n_q_units;
@@ -169,6 +167,11 @@ __global__ __launch_bounds__(256) void quant_qk_i8_kernel(QuantParams p) {
   }
 }
 
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void quant_qk_i8_kernel(QuantParams p) {
+  quant_unit<BF16, D>(p, static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6), threadIdx.x & (kWave - 1));
+}
+
 // ------------------------------------------------------------------ K mean
 constexpr int kMeanChunk = 256;  // rows per stage-1 block
 
@@ -264,7 +267,7 @@ struct VLayoutParams {
 // token-pair dwords in LDS [D][32 pairs], then stores 8 consecutive tokens
 // (16 bytes) per channel row of V_T.  bf16 -> fp16 conversion is fused.
 template <bool BF16, int D>
-__global__ __launch_bounds__(256) void v_layout_kernel(VLayoutParams p) {
+__device__ __forceinline__ void v_layout_tile(const VLayoutParams& p, int64_t blk) {
   constexpr int CPR = D / 8;                        // chunks per token row
   constexpr int PAIRS = kVTile / 2;                 // token pairs per tile
   constexpr int LOAD_TASKS = PAIRS * CPR;           // (pair, chunk) tasks
@@ -275,8 +278,8 @@ __global__ __launch_bounds__(256) void v_layout_kernel(VLayoutParams p) {
   __shared__ __align__(16) uint32_t tile[D * LSTRIDE];
 
   const int t = threadIdx.x;
-  const int64_t bh = blockIdx.x / p.ntiles;
-  const int tile_n = static_cast<int>(blockIdx.x - bh * p.ntiles);
+  const int64_t bh = blk / p.ntiles;
+  const int tile_n = static_cast<int>(blk - bh * p.ntiles);
   const int64_t b = bh / p.h;
   const int64_t h = bh - b * p.h;
   const int n0 = tile_n * kVTile;
@@ -323,6 +326,24 @@ __global__ __launch_bounds__(256) void v_layout_kernel(VLayoutParams p) {
     w.z = s[2];
     w.w = s[3];
     *reinterpret_cast<uint4*>(out + static_cast<int64_t>(d) * p.np + n8 * 8) = w;
+  }
+}
+
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void v_layout_kernel(VLayoutParams p) {
+  v_layout_tile<BF16, D>(p, blockIdx.x);
+}
+
+// K quantisation and the V layout in one launch (the attention kernel
+// quantises Q itself): blocks [0, quant_blocks) quantise four 32-token K units
+// each, the others transform one 64-token V tile each.  Both halves are
+// HBM-bound; one launch saves a launch and lets the two tails overlap.
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void prep_kv_kernel(QuantParams qp, VLayoutParams vp, int32_t quant_blocks) {
+  if (static_cast<int32_t>(blockIdx.x) < quant_blocks) {
+    quant_unit<BF16, D>(qp, static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6), threadIdx.x & (kWave - 1));
+  } else {
+    v_layout_tile<BF16, D>(vp, static_cast<int64_t>(blockIdx.x) - quant_blocks);
   }
 }
 
@@ -518,4 +539,69 @@ extern "C" int sage_v_layout(const void* value, void* value_t, int dtype,
     else v_layout_kernel<false, 64><<<grid, 256, 0, st>>>(p);
   }
   return check_launch("sage_v_layout");
+}
+
+extern "C" int sage_prep_kv_i8(const void* key, const void* value, const void* key_mean, int8_t* k_i8,
+                               float* k_scale, void* value_t, int dtype, int64_t batch, int64_t kv_heads,
+                               int64_t kv_len, int64_t head_dim, int64_t k_stride_b, int64_t k_stride_h,
+                               int64_t k_stride_n, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n,
+                               void* stream) {
+  clear_error();
+  int rc;
+  if ((rc = check_dtype(dtype)) || (rc = check_head_dim(head_dim))) return rc;
+  if (batch < 0 || kv_heads <= 0 || kv_len < 0)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_prep_kv_i8: negative or zero size");
+  if (batch == 0 || kv_len == 0) return SAGE_OK;
+  if (kv_len > INT32_MAX || kv_heads > INT32_MAX ||
+      batch * kv_heads * (sage_v_layout_padded_len(kv_len) / kVTile) > INT32_MAX / 2)
+    return set_error(SAGE_ERR_UNSUPPORTED, "sage_prep_kv_i8: sizes beyond grid limits");
+  if (!key || !value || !k_i8 || !k_scale || !value_t)
+    return set_error(SAGE_ERR_INVALID_ARG, "sage_prep_kv_i8: null key/value/k_i8/k_scale/value_t");
+  if ((rc = check_strides("key", key, k_stride_b, k_stride_h, k_stride_n))) return rc;
+  if ((rc = check_strides("value", value, v_stride_b, v_stride_h, v_stride_n))) return rc;
+  if (key_mean && !aligned(key_mean, 16))
+    return set_error(SAGE_ERR_ALIGNMENT, "key_mean: base pointer must be 16-byte aligned");
+  if (!aligned(k_i8, 8) || !aligned(k_scale, 4) || !aligned(value_t, 16))
+    return set_error(SAGE_ERR_ALIGNMENT,
+                     "sage_prep_kv_i8: k_i8 needs 8-byte, k_scale 4-byte, value_t 16-byte alignment");
+  QuantParams qp = {};
+  qp.k = key;
+  qp.k_mean = key_mean;
+  qp.k8 = k_i8;
+  qp.k_scale = k_scale;
+  qp.k_sb = k_stride_b;
+  qp.k_sh = k_stride_h;
+  qp.k_sn = k_stride_n;
+  qp.hq = 1;
+  qp.hkv = static_cast<int32_t>(kv_heads);
+  qp.sk = static_cast<int32_t>(kv_len);
+  qp.k_units = static_cast<int32_t>(cdiv(kv_len, 32));
+  qp.k_groups = static_cast<int32_t>(cdiv(kv_len, kKGroup));
+  qp.n_q_units = 0;
+  qp.n_units = batch * kv_heads * qp.k_units;
+  qp.s = 1.0f;
+  VLayoutParams vp;
+  vp.v = value;
+  vp.vt = static_cast<uint16_t*>(value_t);
+  vp.sb = v_stride_b;
+  vp.sh = v_stride_h;
+  vp.sn = v_stride_n;
+  vp.np = sage_v_layout_padded_len(kv_len);
+  vp.h = static_cast<int32_t>(kv_heads);
+  vp.s = static_cast<int32_t>(kv_len);
+  vp.ntiles = static_cast<int32_t>(vp.np / kVTile);
+  const int64_t quant_blocks = cdiv(qp.n_units, 4);
+  const int64_t blocks = quant_blocks + batch * kv_heads * vp.ntiles;
+  if (blocks > INT32_MAX) return set_error(SAGE_ERR_UNSUPPORTED, "sage_prep_kv_i8: grid too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  const int32_t qb = static_cast<int32_t>(quant_blocks);
+  if (dtype == SAGE_DTYPE_BF16) {
+    if (head_dim == 128) prep_kv_kernel<true, 128><<<grid, block, 0, st>>>(qp, vp, qb);
+    else prep_kv_kernel<true, 64><<<grid, block, 0, st>>>(qp, vp, qb);
+  } else {
+    if (head_dim == 128) prep_kv_kernel<false, 128><<<grid, block, 0, st>>>(qp, vp, qb);
+    else prep_kv_kernel<false, 64><<<grid, block, 0, st>>>(qp, vp, qb);
+  }
+  return check_launch("sage_prep_kv_i8");
 }

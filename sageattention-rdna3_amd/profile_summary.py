@@ -15,8 +15,8 @@ import json
 import sys
 
 COPY_BYTES = 1 << 30
-KERNELS = ("attn_fwd_kernel", "quant_qk_i8_kernel", "v_layout_kernel", "k_mean_partial_kernel",
-           "k_mean_final_kernel")
+KERNELS = ("attn_fwd_kernel", "prep_kv_kernel", "quant_qk_i8_kernel", "v_layout_kernel", "k_mean_partial_kernel",
+           "k_mean_final_kernel", "attn_merge_kernel")
 
 
 def short_name(name):

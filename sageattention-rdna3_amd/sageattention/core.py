@@ -124,13 +124,12 @@ def sageattn(
     v = _vector_ready(v)
     o = torch.empty_like(q)
 
-    # V transform: fp16 V_T [B,Hkv,D,ceil64(Sk)] zero padded (core.py:145-152,171-180)
-    padded_n = (Sk + 63) // 64 * 64
-    v_t = torch.empty(B, Hkv, D, padded_n, device=q.device, dtype=torch.float16)
-    ops.v_transpose(v, v_t, layout_code)
     lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
 
     if use_direct_path(D, Sq, Sk, bool(is_causal), tensor_layout):
+        # V transform: fp16 V_T [B,Hkv,D,ceil64(Sk)] zero padded (core.py:145-152,171-180)
+        v_t = torch.empty(B, Hkv, D, (Sk + 63) // 64 * 64, device=q.device, dtype=torch.float16)
+        ops.v_transpose(v, v_t, layout_code)
         # direct kernel reads Q and K in place (core.py:141-164); K rows must not overlap
         k_token_stride = k.stride(2) if layout_code == ops.HND else k.stride(1)
         if k_token_stride < D:
@@ -147,9 +146,10 @@ def sageattn(
         k_mean = ops.mean_seq(k, layout_code)
     else:
         k_mean = torch.empty(0, device=q.device, dtype=q.dtype)
-    # K is quantised by its own kernel; Q is quantised inside the attention kernel (the same q_int8
-    # and q_scale as quant_qk_int8 would produce, so the same output, without the int8 Q round trip)
-    k_int8, k_scale = ops.quant_k_int8(k, k_mean, layout_code)
+    # K quantisation and the V transform in one launch; Q is quantised inside the attention kernel (the
+    # same q_int8 and q_scale as quant_qk_int8 would produce, so the same output, without the int8 Q
+    # round trip)
+    k_int8, k_scale, v_t = ops.prep_kv_int8(k, v, k_mean, layout_code)
     # return_lse: the reference returns a zero placeholder (core.py:203-211); the fused kernel writes
     # the real log-sum-exp of each row (natural log, scaled scores; -inf for a row without keys)
     ops.qk_int8_sv_bf16_attn_qfused_t(q, k_int8, v_t, o, k_scale, layout_code, int(is_causal), sm_scale,

@@ -109,6 +109,31 @@ def quant_k_int8(key: torch.Tensor, key_mean: torch.Tensor, tensor_layout: int) 
     return [k8, ks]
 
 
+def prep_kv_int8(key: torch.Tensor, value: torch.Tensor, key_mean: torch.Tensor,
+                 tensor_layout: int) -> List[torch.Tensor]:
+    """:func:`quant_k_int8` and :func:`v_transpose` in one launch -> [k_int8, k_scale, value_t], the
+    same tensors bit for bit (this build's fusion of the K half of the reference's quant_qk_int8 with
+    its v_transpose, for :func:`qk_int8_sv_bf16_attn_qfused_t`)."""
+    (B, Hkv, Sk, D), (ksb, ksh, ksn) = _bhnd(key, tensor_layout)
+    (Bv, Hv, Sv, Dv), (vsb, vsh, vsn) = _bhnd(value, tensor_layout)
+    if (Bv, Hv, Sv, Dv) != (B, Hkv, Sk, D) or value.dtype != key.dtype:
+        raise ValueError("key and value must have the same shape and dtype")
+    dev = key.device
+    k8 = torch.empty((B, Hkv, Sk, D), dtype=torch.int8, device=dev)
+    ks = torch.empty((B, Hkv, (Sk + 15) // 16), dtype=torch.float32, device=dev)
+    vt = torch.empty((B, Hkv, D, (Sk + 63) // 64 * 64), dtype=torch.float16, device=dev)
+    has_mean = key_mean is not None and key_mean.numel() > 0
+    if has_mean:
+        if tuple(key_mean.shape) != (B, Hkv, D) or key_mean.dtype != key.dtype:
+            raise ValueError(f"key_mean must be [{B},{Hkv},{D}] of {key.dtype}")
+        key_mean = key_mean.contiguous()
+    mean_ptr = _ptr(key_mean) if has_mean else ctypes.c_void_p(0)
+    with torch.cuda.device(dev):
+        _capi.call("sage_prep_kv_i8", _ptr(key), _ptr(value), mean_ptr, _ptr(k8), _ptr(ks), _ptr(vt),
+                   _dtype_code(key), B, Hkv, Sk, D, ksb, ksh, ksn, vsb, vsh, vsn, _stream(key))
+    return [k8, ks, vt]
+
+
 def v_transpose(value: torch.Tensor, value_t: torch.Tensor, tensor_layout: int) -> torch.Tensor:
     """V -> fp16 V_T [B,H,D,ceil64(N)] written into ``value_t`` (reference
     v_transpose, csrc/attn_gfx11.cu:1889-1935)."""

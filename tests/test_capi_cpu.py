@@ -225,6 +225,37 @@ def test_qfused_zero_work_is_ok(lib):
     assert qfused(lib, B=0, q=NULL) == _capi.OK
 
 
+def prep(lib, **kw):
+    a = dict(k=FAKE, v=FAKE, mean=NULL, k8=FAKE, ks=FAKE, vt=FAKE, dtype=0, B=1, H=2, S=100, D=128,
+             ksb=2 * 100 * 128, ksh=100 * 128, ksn=128, vsb=2 * 100 * 128, vsh=100 * 128, vsn=128, stream=NULL)
+    a.update(kw)
+    return lib.sage_prep_kv_i8(*a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        (dict(dtype=3), _capi.ERR_INVALID_ARG, "dtype"),
+        (dict(D=80), _capi.ERR_UNSUPPORTED, "head_dim"),
+        (dict(H=0), _capi.ERR_INVALID_ARG, "negative or zero"),
+        (dict(v=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(ks=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(k=ODD), _capi.ERR_ALIGNMENT, "key"),
+        (dict(vsn=132), _capi.ERR_ALIGNMENT, "value"),
+        (dict(mean=ODD), _capi.ERR_ALIGNMENT, "key_mean"),
+        (dict(vt=ctypes.c_void_p(0x10008)), _capi.ERR_ALIGNMENT, "value_t"),
+    ],
+)
+def test_prep_kv_validation(lib, kw, code, msg):
+    assert prep(lib, **kw) == code
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_prep_kv_zero_work_is_ok(lib):
+    assert prep(lib, S=0) == _capi.OK
+    assert prep(lib, B=0, k=NULL) == _capi.OK
+
+
 def test_split_workspace_bytes(lib):
     ws = lib.sage_attn_workspace_bytes
     # forced counts: items (B*Hq*ceil(Sq/256)) x splits x 256 rows x (D + 1) fp32

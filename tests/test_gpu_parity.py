@@ -189,6 +189,31 @@ def test_qfused_equals_quant_then_attention(cfg):
     assert torch.equal(lse, lse_ref)
 
 
+@pytest.mark.parametrize("cfg", [c for c in SMALL if c.dtype != "fp32"] + [BASELINE_CONFIGS[2], BASELINE_CONFIGS[3]],
+                         ids=lambda c: c.name)
+def test_prep_kv_equals_quant_and_v_layout(cfg):
+    """K quantisation and the V layout in one launch (what sageattn runs) give the separate kernels'
+    k_int8, k_scale and V_T bit for bit, and these equal the oracle's (layouts, dtypes, smooth_k,
+    ragged lengths, GQA)."""
+    from sageattention import ops
+
+    _say(f"[prep_kv] {cfg}")
+    lay = ops.HND if cfg.layout == "HND" else ops.NHD
+    q, k, v = make_inputs(cfg, seed=10)
+    kd, vd = k.cuda(), v.cuda()
+    mean = ops.mean_seq(kd, lay) if cfg.smooth_k else torch.empty(0, device="cuda", dtype=kd.dtype)
+    k8, ks, vt = ops.prep_kv_int8(kd, vd, mean, lay)
+    k8_ref, ks_ref = ops.quant_k_int8(kd, mean, lay)
+    vt_ref = torch.empty_like(vt)
+    ops.v_transpose(vd, vt_ref, lay)
+    torch.cuda.synchronize()
+    assert torch.equal(k8, k8_ref) and torch.equal(ks, ks_ref) and torch.equal(vt, vt_ref)
+    if cfg.S <= 4096:
+        pro = gpu_prologue(cfg, q, k, v)
+        assert_prologue_exact(cfg, q, k, v, pro)
+        assert torch.equal(k8, pro["k8"]) and torch.equal(vt, pro["v_t"])
+
+
 def test_qfused_large_scales_and_negative_scale():
     """The fused quantiser on the extreme-scale inputs (exact-softmax fallback) and with a negative
     sm_scale (negated q_int8, positive scales), against the two-kernel path."""
