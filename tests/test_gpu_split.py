@@ -225,3 +225,36 @@ def test_split_repeat_is_deterministic_and_causal_ignores_splits():
     c1, l1 = fused_split(ccfg, qd, pro["k8"], pro["k_scale"], pro["v_t"], 1)
     c6, l6 = fused_split(ccfg, qd, pro["k8"], pro["k_scale"], pro["v_t"], 6)
     assert torch.equal(c1, c6) and torch.equal(l1, l6)
+
+
+# ------------------------------------------------------------------ persistent grid (more items than CUs)
+PERSISTENT = [
+    # 300 / 600 q-blocks of one 256-row block each: a persistent grid with 1-3 items per block
+    Config("p_causal_h300", 1, 300, 300, 256, 64, "fp16", "HND", True, False),
+    Config("p_noncausal_gqa_h600", 1, 600, 150, 200, 128, "bf16", "NHD", False, False),
+    Config("p_cross_causal_2x160", 2, 160, 40, 130, 64, "bf16", "HND", True, False, Sq=300),
+    Config("p_smooth_b3", 3, 100, 100, 333, 128, "fp16", "HND", False, True),
+]
+
+
+@pytest.mark.parametrize("cfg", PERSISTENT, ids=lambda c: c.name)
+def test_persistent_grid_all_rows_vs_oracle(cfg):
+    """Launches with more q-blocks than CUs run a persistent grid (static snake schedule over the XCDs);
+    every row of the fused-Q INT8 kernel and of the direct kernel is held to the oracle bar, and the
+    INT8 output equals the two-kernel path bit for bit (each item is computed the same way in any
+    schedule)."""
+    from sageattention import ops
+
+    _say(f"[persistent] {cfg}")
+    q, k, v = make_inputs(cfg, seed=31)
+    pro = gpu_prologue(cfg, q, k, v)
+    qd = q.cuda()
+    o, _ = fused_split(cfg, qd, pro["k8"], pro["k_scale"], pro["v_t"], 1)
+    check_rows_vs_oracle(cfg, pro, o, range(cfg.Hq), np.arange(cfg.q_len), cfg.dtype)
+    o2 = torch.empty_like(qd)
+    ops.qk_int8_sv_bf16_attn_t(pro["q8"], pro["k8"], pro["v_t"], o2, pro["q_scale"], pro["k_scale"], _lay(cfg),
+                               int(cfg.causal), cfg.D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2)
+    od, _ = direct_split(cfg, qd, k.cuda(), pro["v_t"], 1)
+    check_direct_rows(cfg, q, k, pro["v_t"], od, range(cfg.Hq), np.arange(cfg.q_len), cfg.D ** -0.5)
