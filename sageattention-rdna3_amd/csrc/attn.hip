@@ -39,8 +39,14 @@
 //     direct path reads K (and Q) straight from the caller's strided tensors;
 //   * causal: the KV loop stops at the block's last row, masks only on tail /
 //     diagonal tiles;
-//   * block -> work remap keeps consecutive q-blocks of a head on one XCD
-//     (shared L2 for K/V) and issues the heaviest causal blocks first.
+//   * work items (a q-block, or a key range of one for split launches) go to
+//     XCDs in contiguous ranges (consecutive q-blocks of a head share an XCD's
+//     L2 for K/V), heaviest causal blocks first; with more items than CUs a
+//     persistent grid of one block per CU walks a static snake schedule
+//     instead of relying on the hardware dispatcher (see attn_fwd_kernel);
+//   * the epilogue stages each wave's output rows in LDS and writes whole
+//     rows; non-causal launches that leave CUs idle can split key ranges,
+//     merged by attn_merge_kernel with the partial LSEs.
 #include <atomic>
 #include <cmath>
 #include <type_traits>
