@@ -857,6 +857,13 @@ __device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float
     // ST (0..2) is the compile-time stage of the unrolled unmasked loop, so
     // every LDS operand address is a lane offset plus an immediate; ST = -1
     // (masked loop) takes the stage at run time.
+    // causal: a tile whose first key lies past the wave's last row is masked
+    // for all of the wave's rows; its softmax would leave m, l and O as they
+    // are (P = 0), so the wave skips the tile's QK, softmax and P.V while the
+    // loads and barriers stay with the block.  Such tiles are the block's last
+    // (the condition grows with the tile), so a skipped softmax is followed only
+    // by skipped P.Vs and never feeds its stale P fragments to an MFMA.
+    auto dead_tile = [&](int t) __attribute__((always_inline)) { return CAUSAL && kv0 + t * kBN > wrow0 + 31; };
     auto step = [&](int j, int st_rt, auto mask_tag, auto st_tag) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(mask_tag)::value;
       constexpr int ST = decltype(st_tag)::value;
@@ -871,7 +878,7 @@ __device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float
       // scales too large for the conversion-free softmax: the same work in
       // plain order, P.V (reads P) -> softmax (reads S, writes P) -> QK (writes S)
       auto sequential = [&]() __attribute__((always_inline)) {
-        pv_tile<D, QK>(vring + st2 * C::kVStage, om, pf, o);
+        if (!dead_tile(j - 1)) pv_tile<D, QK>(vring + st2 * C::kVStage, om, pf, o);
         auto softmax = [&](auto smask_tag) __attribute__((always_inline)) {
           using SM = TileSoftmax<D, QK, CAUSAL, decltype(smask_tag)::value>;
           SM sm(p, s, ks, qs, kv0 + j * kBN, qrow, hh);
@@ -879,12 +886,14 @@ __device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float
         };
         // this wave's keys of tile j are all live: inside the key range and,
         // causal, left of the wave's first row
-        if (kv0 + j * kBN + kBN - 1 <= (CAUSAL ? min(wrow0, p.sk - 1) : p.sk - 1)) {
+        if (dead_tile(j)) {
+          need = false;  // no softmax: m, l and O stay as they are
+        } else if (kv0 + j * kBN + kBN - 1 <= (CAUSAL ? min(wrow0, p.sk - 1) : p.sk - 1)) {
           softmax(std::false_type{});
         } else {
           softmax(std::true_type{});
         }
-        qk_tile<D, QK>(kread + st1 * C::kKStage, om, qf, s, sinit);
+        if (!dead_tile(j + 1)) qk_tile<D, QK>(kread + st1 * C::kKStage, om, qf, s, sinit);
       };
       if constexpr (!MASKED) {
         using SM = TileSoftmax<D, QK, CAUSAL, false, true>;
@@ -920,7 +929,7 @@ __device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float
     // last P.V: V_{ntiles-1} sits in stage (ntiles-1) % 3
     wait_loads_barrier<C::kStepLoads>();
     rescale_o();
-    pv_tile<D, QK>(vring + (st == 0 ? 2 : st - 1) * C::kVStage, om, pf, o);
+    if (!dead_tile(ntiles - 1)) pv_tile<D, QK>(vring + (st == 0 ? 2 : st - 1) * C::kVStage, om, pf, o);
     // loads of tiles past the end may still be in flight into this block's LDS
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
