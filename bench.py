@@ -220,7 +220,7 @@ REFERENCE_SHAPES = [
 ]
 
 
-def reference_shapes_probe(dev, n, names=None):
+def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
     """Whole ``sageattn`` calls (quantisation, V layout, attention) at the reference's benchmark shapes
     (``names``: a subset), with the library's key-split plan and with splitting switched off
     (SAGEATTN_KV_SPLITS=1)."""
@@ -237,7 +237,7 @@ def reference_shapes_probe(dev, n, names=None):
             cfg = (B, H, H, S, D, dt, "HND", False, False)
             q, k, v = make_inputs(cfg, dev)
             res = {}
-            for mode in ("auto", "1"):
+            for mode in modes:
                 if mode == "auto":
                     os.environ.pop("SAGEATTN_KV_SPLITS", None)
                 else:
@@ -255,12 +255,15 @@ def reference_shapes_probe(dev, n, names=None):
                 res[mode] = e0.elapsed_time(e1) / n
             whole, splits = _capi.split_plan(True, B, H, S, S, D, False, 0)
             flops = attn_ops(B, H, S, S, D, False)
-            out.append({"shape": name, "B": B, "H": H, "S": S, "D": D, "dtype": dt,
-                        "plan": {"whole_qblocks": whole, "splits": splits},
-                        "ms": round(res["auto"], 4), "tops": round(flops / (res["auto"] * 1e-3) / 1e12, 1),
-                        "ms_unsplit": round(res["1"], 4)})
-            log(f"[bench] {name}: sageattn {res['auto']:.4f} ms ({out[-1]['tops']} TOPS), unsplit "
-                f"{res['1']:.4f} ms, plan {whole} whole + splits of {splits}")
+            row = {"shape": name, "B": B, "H": H, "S": S, "D": D, "dtype": dt,
+                   "plan": {"whole_qblocks": whole, "splits": splits}}
+            if "auto" in res:
+                row.update(ms=round(res["auto"], 4), tops=round(flops / (res["auto"] * 1e-3) / 1e12, 1))
+            if "1" in res:
+                row.update(ms_unsplit=round(res["1"], 4))
+            out.append(row)
+            log(f"[bench] {name}: " + ", ".join(f"{'sageattn' if m == 'auto' else 'unsplit'} {t:.4f} ms"
+                                                 for m, t in res.items()) + f", plan {whole} whole + splits of {splits}")
             del q, k, v
     finally:
         if saved is None:
@@ -283,6 +286,8 @@ def main():
     ap.add_argument("--reference-shapes", default=None, metavar="NAMES",
                     help="only time sageattn at these reference benchmark shapes (comma list, or 'all'), "
                          "print them as one JSON line and exit; for rocprofv3 runs of the split path")
+    ap.add_argument("--reference-modes", default="auto,1", metavar="MODES",
+                    help="with --reference-shapes: 'auto' (the library's key-split plan) and/or '1' (unsplit)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="launch each path kernel --steps times plus a 1 GiB device copy (the HBM-counter "
                          "calibration) and exit; for rocprofv3 --pmc runs")
@@ -311,7 +316,11 @@ def main():
         unknown = (names or set()) - {x[0] for x in REFERENCE_SHAPES}
         if unknown:
             sys.exit(f"unknown reference shapes: {sorted(unknown)}")
-        print(json.dumps({"reference_shapes": reference_shapes_probe(dev, max(args.steps, 10), names)}), flush=True)
+        modes = tuple(m for m in args.reference_modes.split(",") if m)
+        if not modes or any(m not in ("auto", "1") for m in modes):
+            sys.exit("--reference-modes takes 'auto' and/or '1'")
+        print(json.dumps({"reference_shapes": reference_shapes_probe(dev, max(args.steps, 10), names, modes)}),
+              flush=True)
         return
 
     q, k, v = make_inputs(cfg, dev)
