@@ -209,33 +209,52 @@ def direct_probe(dev, n):
     }
 
 
-# the reference's own benchmark shapes (benchmark_attn/benchmark_attn-result-native.txt, all non-causal
-# HND self-attention): name, B, H, S, D, dtype
+# the reference's own benchmark shapes (benchmark_attn/benchmark_attn.py:143-174, results in
+# benchmark_attn-result-native.txt; all non-causal HND, h_q == h_kv): name, B, H, Sq, Sk, D, dtype.  The
+# long self-attention shapes take the INT8 path, the short and cross-attention ones (kv 77, 154, 512,
+# self-attention up to 2304) the direct path, as the reference dispatches them.
 REFERENCE_SHAPES = [
-    ("SDXL01", 1, 10, 4096, 64, "fp16"), ("SDXL07", 1, 10, 6144, 64, "fp16"), ("SDXL13", 1, 10, 9216, 64, "fp16"),
-    ("SDXLVAE01", 1, 4, 16384, 128, "fp16"), ("SDXLVAE02", 1, 4, 24576, 128, "fp16"),
-    ("Anima01", 1, 16, 4096, 128, "bf16"), ("AnimaVAE01", 1, 3, 16384, 128, "bf16"),
-    ("Anima03", 1, 16, 6144, 128, "bf16"), ("AnimaVAE02", 1, 3, 24576, 128, "bf16"),
-    ("Anima05", 1, 16, 9216, 128, "bf16"),
+    ("SDXL01", 1, 10, 4096, 4096, 64, "fp16"), ("SDXL02", 1, 10, 4096, 77, 64, "fp16"),
+    ("SDXL03", 1, 10, 4096, 154, 64, "fp16"), ("SDXL04", 1, 20, 1024, 1024, 64, "fp16"),
+    ("SDXL05", 1, 20, 1024, 77, 64, "fp16"), ("SDXL06", 1, 20, 1024, 154, 64, "fp16"),
+    ("SDXLVAE01", 1, 4, 16384, 16384, 128, "fp16"), ("SDXL07", 1, 10, 6144, 6144, 64, "fp16"),
+    ("SDXL08", 1, 10, 6144, 77, 64, "fp16"), ("SDXL09", 1, 10, 6144, 154, 64, "fp16"),
+    ("SDXL10", 1, 20, 1536, 1536, 64, "fp16"), ("SDXL11", 1, 20, 1536, 77, 64, "fp16"),
+    ("SDXL12", 1, 20, 1536, 154, 64, "fp16"), ("SDXLVAE02", 1, 4, 24576, 24576, 128, "fp16"),
+    ("SDXL13", 1, 10, 9216, 9216, 64, "fp16"), ("SDXL14", 1, 10, 9216, 77, 64, "fp16"),
+    ("SDXL15", 1, 10, 9216, 154, 64, "fp16"), ("SDXL16", 1, 20, 2304, 2304, 64, "fp16"),
+    ("SDXL17", 1, 20, 2304, 77, 64, "fp16"), ("SDXL18", 1, 20, 2304, 154, 64, "fp16"),
+    ("Anima01", 1, 16, 4096, 4096, 128, "bf16"), ("Anima02", 1, 16, 4096, 512, 128, "bf16"),
+    ("AnimaVAE01", 1, 3, 16384, 16384, 128, "bf16"), ("Anima03", 1, 16, 6144, 6144, 128, "bf16"),
+    ("Anima04", 1, 16, 6144, 512, 128, "bf16"), ("AnimaVAE02", 1, 3, 24576, 24576, 128, "bf16"),
+    ("Anima05", 1, 16, 9216, 9216, 128, "bf16"), ("Anima06", 1, 16, 9216, 512, 128, "bf16"),
 ]
 
 
 def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
-    """Whole ``sageattn`` calls (quantisation, V layout, attention) at the reference's benchmark shapes
-    (``names``: a subset), with the library's key-split plan and with splitting switched off
-    (SAGEATTN_KV_SPLITS=1)."""
+    """Whole ``sageattn`` calls (the reference's dispatch: quantisation, V layout and INT8 attention, or
+    V layout and the direct kernel) at the reference's benchmark shapes (``names``: a subset), back to
+    back on one stream, with the library's key-split plan and with splitting switched off
+    (SAGEATTN_KV_SPLITS=1).  ``ms`` is the time per call as a caller sees it: for the smallest
+    shapes the host's issue time per call, when it exceeds the GPU's."""
     import torch
 
     from sageattention import _capi, sageattn
+    from sageattention.core import use_direct_path
 
     out = []
     saved = os.environ.get("SAGEATTN_KV_SPLITS")
     try:
-        for name, B, H, S, D, dt in REFERENCE_SHAPES:
+        for name, B, H, Sq, Sk, D, dt in REFERENCE_SHAPES:
             if names is not None and name not in names:
                 continue
-            cfg = (B, H, H, S, D, dt, "HND", False, False)
-            q, k, v = make_inputs(cfg, dev)
+            dtype = torch.bfloat16 if dt == "bf16" else torch.float16
+            g = torch.Generator(device=dev).manual_seed(0)
+            q = torch.randn((B, H, Sq, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            k = torch.randn((B, H, Sk, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            v = torch.randn((B, H, Sk, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            direct = use_direct_path(D, Sq, Sk, False, "HND")
+            calls = n if Sq * Sk >= 1 << 24 else max(n, 200)  # enough calls to time the short shapes
             res = {}
             for mode in modes:
                 if mode == "auto":
@@ -248,22 +267,23 @@ def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)
                 e0.record()
-                for _ in range(n):
+                for _ in range(calls):
                     sageattn(q, k, v, tensor_layout="HND", is_causal=False)
                 e1.record()
                 e1.synchronize()
-                res[mode] = e0.elapsed_time(e1) / n
-            whole, splits = _capi.split_plan(True, B, H, S, S, D, False, 0)
-            flops = attn_ops(B, H, S, S, D, False)
-            row = {"shape": name, "B": B, "H": H, "S": S, "D": D, "dtype": dt,
-                   "plan": {"whole_qblocks": whole, "splits": splits}}
+                res[mode] = e0.elapsed_time(e1) / calls
+            whole, splits = _capi.split_plan(not direct, B, H, Sq, Sk, D, False, 0)
+            flops = attn_ops(B, H, Sq, Sk, D, False)
+            row = {"shape": name, "B": B, "H": H, "Sq": Sq, "Sk": Sk, "D": D, "dtype": dt,
+                   "path": "direct" if direct else "int8", "plan": {"whole_qblocks": whole, "splits": splits}}
             if "auto" in res:
                 row.update(ms=round(res["auto"], 4), tops=round(flops / (res["auto"] * 1e-3) / 1e12, 1))
             if "1" in res:
                 row.update(ms_unsplit=round(res["1"], 4))
             out.append(row)
-            log(f"[bench] {name}: " + ", ".join(f"{'sageattn' if m == 'auto' else 'unsplit'} {t:.4f} ms"
-                                                 for m, t in res.items()) + f", plan {whole} whole + splits of {splits}")
+            log(f"[bench] {name} ({row['path']}): " +
+                ", ".join(f"{'sageattn' if m == 'auto' else 'unsplit'} {t:.4f} ms" for m, t in res.items()) +
+                f", plan {whole} whole + splits of {splits}")
             del q, k, v
     finally:
         if saved is None:

@@ -8,7 +8,9 @@ stream.  ``tensor_layout`` is the reference's integer code: 1 = HND
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import functools
 from typing import List, Optional
 
 import torch
@@ -32,17 +34,40 @@ def _bhnd(t: torch.Tensor, tensor_layout: int):
     """(B, H, N, D) sizes and (stride_b, stride_h, stride_n) of a 4-D tensor."""
     if t.dim() != 4:
         raise ValueError(f"expected a 4-D tensor, got shape {tuple(t.shape)}")
+    n, st = t.shape, t.stride()
     if tensor_layout == HND:
-        return (t.size(0), t.size(1), t.size(2), t.size(3)), (t.stride(0), t.stride(1), t.stride(2))
-    return (t.size(0), t.size(2), t.size(1), t.size(3)), (t.stride(0), t.stride(2), t.stride(1))
+        return (n[0], n[1], n[2], n[3]), (st[0], st[1], st[2])
+    return (n[0], n[2], n[1], n[3]), (st[0], st[2], st[1])
 
 
-def _stream(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+# the raw handle of a device's current stream; the public torch.cuda.current_stream(device) builds a
+# Stream object first (~1.7 us a call, against ~0.1 us)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def _ptr(t: torch.Tensor):
-    return ctypes.c_void_p(t.data_ptr())
+def _stream(t: torch.Tensor) -> int:
+    """Handle of the current HIP stream on ``t``'s device (the stream every launch is ordered on)."""
+    idx = t.device.index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _on_device(dev: torch.device):
+    """``torch.cuda.device(dev)``, or nothing when ``dev`` is already current (the common case; the
+    context manager costs ~1 us per use).  The library reads the current device for its CU count."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+_NULL = None  # a null pointer argument
 
 
 def mean_seq(input: torch.Tensor, tensor_layout: int) -> torch.Tensor:
@@ -53,7 +78,7 @@ def mean_seq(input: torch.Tensor, tensor_layout: int) -> torch.Tensor:
     lib = _capi.load()
     ws_bytes = lib.sage_k_mean_workspace_bytes(B, H, S, D)
     ws = torch.empty((max(ws_bytes, 4) + 3) // 4, dtype=torch.float32, device=input.device)
-    with torch.cuda.device(input.device):
+    with _on_device(input.device):
         _capi.call("sage_k_mean", _ptr(input), _ptr(out), _ptr(ws), _dtype_code(input),
                    B, H, S, D, sb, sh, sn, _stream(input))
     return out
@@ -80,8 +105,8 @@ def quant_qk_int8(query: torch.Tensor, key: torch.Tensor, key_mean: torch.Tensor
         if tuple(key_mean.shape) != (B, Hkv, D) or key_mean.dtype != key.dtype:
             raise ValueError(f"key_mean must be [{B},{Hkv},{D}] of {key.dtype}")
         key_mean = key_mean.contiguous()
-    mean_ptr = _ptr(key_mean) if has_mean else ctypes.c_void_p(0)
-    with torch.cuda.device(dev):
+    mean_ptr = _ptr(key_mean) if has_mean else _NULL
+    with _on_device(dev):
         _capi.call("sage_quant_qk_i8", _ptr(query), _ptr(key), mean_ptr,
                    _ptr(q8), _ptr(qs), _ptr(k8), _ptr(ks), _dtype_code(query),
                    B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, ksb, ksh, ksn,
@@ -101,9 +126,9 @@ def quant_k_int8(key: torch.Tensor, key_mean: torch.Tensor, tensor_layout: int) 
         if tuple(key_mean.shape) != (B, Hkv, D) or key_mean.dtype != key.dtype:
             raise ValueError(f"key_mean must be [{B},{Hkv},{D}] of {key.dtype}")
         key_mean = key_mean.contiguous()
-    mean_ptr = _ptr(key_mean) if has_mean else ctypes.c_void_p(0)
-    null = ctypes.c_void_p(0)
-    with torch.cuda.device(dev):
+    mean_ptr = _ptr(key_mean) if has_mean else _NULL
+    null = _NULL
+    with _on_device(dev):
         _capi.call("sage_quant_qk_i8", null, _ptr(key), mean_ptr, null, null, _ptr(k8), _ptr(ks),
                    _dtype_code(key), B, Hkv, Hkv, 0, Sk, D, 0, 0, 0, ksb, ksh, ksn, 1.0, _stream(key))
     return [k8, ks]
@@ -114,38 +139,47 @@ def prep_kv_int8(key: torch.Tensor, value: torch.Tensor, key_mean: torch.Tensor,
     """:func:`quant_k_int8` and :func:`v_transpose` in one launch -> [k_int8, k_scale, value_t], the
     same tensors bit for bit (this build's fusion of the K half of the reference's quant_qk_int8 with
     its v_transpose, for :func:`qk_int8_sv_bf16_attn_qfused_t`)."""
-    (B, Hkv, Sk, D), (ksb, ksh, ksn) = _bhnd(key, tensor_layout)
-    (Bv, Hv, Sv, Dv), (vsb, vsh, vsn) = _bhnd(value, tensor_layout)
+    (B, Hkv, Sk, D), kst = _bhnd(key, tensor_layout)
+    (Bv, Hv, Sv, Dv), vst = _bhnd(value, tensor_layout)
     if (Bv, Hv, Sv, Dv) != (B, Hkv, Sk, D) or value.dtype != key.dtype:
         raise ValueError("key and value must have the same shape and dtype")
-    dev = key.device
-    k8 = torch.empty((B, Hkv, Sk, D), dtype=torch.int8, device=dev)
-    ks = torch.empty((B, Hkv, (Sk + 15) // 16), dtype=torch.float32, device=dev)
-    vt = torch.empty((B, Hkv, D, (Sk + 63) // 64 * 64), dtype=torch.float16, device=dev)
     has_mean = key_mean is not None and key_mean.numel() > 0
     if has_mean:
         if tuple(key_mean.shape) != (B, Hkv, D) or key_mean.dtype != key.dtype:
             raise ValueError(f"key_mean must be [{B},{Hkv},{D}] of {key.dtype}")
         key_mean = key_mean.contiguous()
-    mean_ptr = _ptr(key_mean) if has_mean else ctypes.c_void_p(0)
-    with torch.cuda.device(dev):
-        _capi.call("sage_prep_kv_i8", _ptr(key), _ptr(value), mean_ptr, _ptr(k8), _ptr(ks), _ptr(vt),
-                   _dtype_code(key), B, Hkv, Sk, D, ksb, ksh, ksn, vsb, vsh, vsn, _stream(key))
+    with _on_device(key.device):
+        return _prep_kv_launch(key, value, key_mean if has_mean else None, B, Hkv, Sk, D, kst, vst, _stream(key))
+
+
+def _prep_kv_launch(key, value, key_mean, B, Hkv, Sk, D, kst, vst, stream) -> List[torch.Tensor]:
+    """Allocate [k_int8, k_scale, value_t] and launch sage_prep_kv_i8 (arguments already checked)."""
+    dev = key.device
+    k8 = torch.empty((B, Hkv, Sk, D), dtype=torch.int8, device=dev)
+    ks = torch.empty((B, Hkv, (Sk + 15) // 16), dtype=torch.float32, device=dev)
+    vt = torch.empty((B, Hkv, D, (Sk + 63) // 64 * 64), dtype=torch.float16, device=dev)
+    _capi.call("sage_prep_kv_i8", key.data_ptr(), value.data_ptr(),
+               key_mean.data_ptr() if key_mean is not None else _NULL, k8.data_ptr(), ks.data_ptr(),
+               vt.data_ptr(), _dtype_code(key), B, Hkv, Sk, D, *kst, *vst, stream)
     return [k8, ks, vt]
 
 
 def v_transpose(value: torch.Tensor, value_t: torch.Tensor, tensor_layout: int) -> torch.Tensor:
     """V -> fp16 V_T [B,H,D,ceil64(N)] written into ``value_t`` (reference
     v_transpose, csrc/attn_gfx11.cu:1889-1935)."""
-    (B, H, S, D), (sb, sh, sn) = _bhnd(value, tensor_layout)
+    (B, H, S, D), vst = _bhnd(value, tensor_layout)
     NP = (S + 63) // 64 * 64
     if (tuple(value_t.shape) != (B, H, D, NP) or value_t.dtype != torch.float16
             or not value_t.is_contiguous()):
         raise ValueError(f"value_t must be contiguous fp16 [{B},{H},{D},{NP}]")
-    with torch.cuda.device(value.device):
-        _capi.call("sage_v_layout", _ptr(value), _ptr(value_t), _dtype_code(value),
-                   B, H, S, D, sb, sh, sn, _stream(value))
+    with _on_device(value.device):
+        _v_layout_launch(value, value_t, B, H, S, D, vst, _stream(value))
     return value_t
+
+
+def _v_layout_launch(value, value_t, B, H, S, D, vst, stream) -> None:
+    _capi.call("sage_v_layout", value.data_ptr(), value_t.data_ptr(), _dtype_code(value), B, H, S, D, *vst,
+               stream)
 
 
 def qk_int8_sv_bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
@@ -177,16 +211,23 @@ def qk_int8_sv_bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.
     if lse is not None:
         if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
             raise ValueError(f"lse must be contiguous fp32 [{B},{Hq},{Sq}]")
-        with torch.cuda.device(query.device):
+        with _on_device(query.device):
             _capi.call("sage_attn_i8_fwd_lse", _ptr(query), _ptr(key), _ptr(value), _ptr(output), _ptr(lse),
                        _ptr(q_scale), _ptr(k_scale), _dtype_code(output),
                        B, Hq, Hkv, Sq, Sk, D, osb, osh, osn, int(bool(is_causal)), _stream(query))
         return output
-    with torch.cuda.device(query.device):
+    with _on_device(query.device):
         _capi.call("sage_attn_i8_fwd", _ptr(query), _ptr(key), _ptr(value), _ptr(output),
                    _ptr(q_scale), _ptr(k_scale), _dtype_code(output),
                    B, Hq, Hkv, Sq, Sk, D, osb, osh, osn, int(bool(is_causal)), _stream(query))
     return output
+
+
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(quantized: int, B: int, Hq: int, Sq: int, Sk: int, D: int, is_causal: int, num_splits: int,
+                     device_index: int) -> int:
+    # the plan depends on the shape and on the device (its CU count) only
+    return _capi.query("sage_attn_workspace_bytes", quantized, B, Hq, Sq, Sk, D, is_causal, num_splits)
 
 
 def _split_workspace(quantized: bool, B: int, Hq: int, Sq: int, Sk: int, D: int, is_causal: int,
@@ -195,12 +236,14 @@ def _split_workspace(quantized: bool, B: int, Hq: int, Sq: int, Sk: int, D: int,
     with ``device`` current: the library's split choice depends on its CU count."""
     if not 0 <= int(num_splits) <= _capi.MAX_KV_SPLITS:
         raise ValueError(f"num_splits must be in [0, {_capi.MAX_KV_SPLITS}], got {num_splits}")
-    nbytes = _capi.query("sage_attn_workspace_bytes", int(quantized), B, Hq, Sq, Sk, D, int(bool(is_causal)),
-                         int(num_splits))
+    if is_causal:
+        return None, _NULL, 0  # causal launches never split
+    nbytes = _workspace_bytes(int(quantized), B, Hq, Sq, Sk, D, 0, int(num_splits),
+                              device.index if device.index is not None else torch.cuda.current_device())
     if nbytes == 0:
-        return None, ctypes.c_void_p(0), 0
+        return None, _NULL, 0
     ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    return ws, _ptr(ws), nbytes
+    return ws, ws.data_ptr(), nbytes
 
 
 def _direct_attn_t(op: str, want: torch.dtype, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
@@ -211,28 +254,34 @@ def _direct_attn_t(op: str, want: torch.dtype, query: torch.Tensor, key: torch.T
             raise ValueError(f"{op}: {name} must be {want}, got {t.dtype}")
         if t.dim() != 4 or t.stride(-1) != 1:
             raise ValueError(f"{op}: {name} must be 4-D with a contiguous head_dim axis")
-    (B, Hq, Sq, D), (qsb, qsh, qsn) = _bhnd(query, tensor_layout)
-    (Bk, Hkv, Sk, Dk), (ksb, ksh, ksn) = _bhnd(key, tensor_layout)
+    (B, Hq, Sq, D), qst = _bhnd(query, tensor_layout)
+    (Bk, Hkv, Sk, Dk), kst = _bhnd(key, tensor_layout)
     if Bk != B or Dk != D:
         raise ValueError(f"{op}: query {tuple(query.shape)} and key {tuple(key.shape)} disagree")
     NP = (Sk + 63) // 64 * 64
     if tuple(value.shape) != (B, Hkv, D, NP) or value.dtype != torch.float16 or not value.is_contiguous():
         raise ValueError(f"{op}: value must be contiguous fp16 V_T [{B},{Hkv},{D},{NP}]")
-    (Bo, Ho, So, Do), (osb, osh, osn) = _bhnd(output, tensor_layout)
+    (Bo, Ho, So, Do), ost = _bhnd(output, tensor_layout)
     if (Bo, Ho, So, Do) != (B, Hq, Sq, D):
         raise ValueError(f"{op}: output shape does not match the query")
-    lse_ptr = ctypes.c_void_p(0)
     if lse is not None:
         if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
             raise ValueError(f"{op}: lse must be contiguous fp32 [{B},{Hq},{Sq}]")
-        lse_ptr = _ptr(lse)
-    with torch.cuda.device(query.device):
-        ws, ws_ptr, ws_bytes = _split_workspace(False, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
-        _capi.call("sage_attn_direct_fwd", _ptr(query), _ptr(key), _ptr(value), _ptr(output), lse_ptr,
-                   _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, ksb, ksh, ksn, osb, osh, osn,
-                   int(bool(is_causal)), float(sm_scale), int(num_splits), ws_ptr, ws_bytes, _stream(query))
-        del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
+    with _on_device(query.device):
+        _direct_launch(query, key, value, output, lse, B, Hq, Hkv, Sq, Sk, D, qst, kst, ost, is_causal,
+                       sm_scale, num_splits, _stream(query))
     return output
+
+
+def _direct_launch(query, key, value_t, output, lse, B, Hq, Hkv, Sq, Sk, D, qst, kst, ost, is_causal, sm_scale,
+                   num_splits, stream) -> None:
+    """sage_attn_direct_fwd on checked arguments, with the key-split workspace when the plan needs one
+    (the device must be current)."""
+    ws, ws_ptr, ws_bytes = _split_workspace(False, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
+    _capi.call("sage_attn_direct_fwd", query.data_ptr(), key.data_ptr(), value_t.data_ptr(), output.data_ptr(),
+               lse.data_ptr() if lse is not None else _NULL, _dtype_code(query), B, Hq, Hkv, Sq, Sk, D,
+               *qst, *kst, *ost, int(bool(is_causal)), float(sm_scale), int(num_splits), ws_ptr, ws_bytes, stream)
+    del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
 
 
 def fp16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, output: torch.Tensor,
@@ -268,7 +317,7 @@ def qk_int8_sv_bf16_attn_qfused_t(query: torch.Tensor, key: torch.Tensor, value:
     from :func:`quant_k_int8`, ``value`` is the fp16 V_T.  ``num_splits`` as in :func:`fp16_attn_t`
     (the bit-identity with the two-kernel path holds for unsplit launches).  This build's fusion; no
     single reference op."""
-    (B, Hq, Sq, D), (qsb, qsh, qsn) = _bhnd(query, tensor_layout)
+    (B, Hq, Sq, D), qst = _bhnd(query, tensor_layout)
     if query.stride(-1) != 1 or output.dtype != query.dtype:
         raise ValueError("query needs a contiguous head_dim axis and the output's dtype")
     Bk, Hkv, Sk, Dk = key.shape
@@ -280,18 +329,25 @@ def qk_int8_sv_bf16_attn_qfused_t(query: torch.Tensor, key: torch.Tensor, value:
     if (tuple(k_scale.shape) != (B, Hkv, (Sk + 15) // 16) or k_scale.dtype != torch.float32
             or not k_scale.is_contiguous()):
         raise ValueError("k_scale must be contiguous fp32 [B,Hkv,ceil(Sk/16)]")
-    (Bo, Ho, So, Do), (osb, osh, osn) = _bhnd(output, tensor_layout)
+    (Bo, Ho, So, Do), ost = _bhnd(output, tensor_layout)
     if (Bo, Ho, So, Do) != (B, Hq, Sq, D) or output.stride(-1) != 1:
         raise ValueError("output shape does not match the query")
-    lse_ptr = ctypes.c_void_p(0)
     if lse is not None:
         if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
             raise ValueError(f"lse must be contiguous fp32 [{B},{Hq},{Sq}]")
-        lse_ptr = _ptr(lse)
-    with torch.cuda.device(query.device):
-        ws, ws_ptr, ws_bytes = _split_workspace(True, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
-        _capi.call("sage_attn_i8_fwd_qfused", _ptr(query), _ptr(key), _ptr(value), _ptr(output), lse_ptr,
-                   _ptr(k_scale), _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, qsb, qsh, qsn, osb, osh, osn,
-                   int(bool(is_causal)), float(sm_scale), int(num_splits), ws_ptr, ws_bytes, _stream(query))
-        del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
+    with _on_device(query.device):
+        _qfused_launch(query, key, value, output, lse, k_scale, B, Hq, Hkv, Sq, Sk, D, qst, ost, is_causal,
+                       sm_scale, num_splits, _stream(query))
     return output
+
+
+def _qfused_launch(query, key, value_t, output, lse, k_scale, B, Hq, Hkv, Sq, Sk, D, qst, ost, is_causal,
+                   sm_scale, num_splits, stream) -> None:
+    """sage_attn_i8_fwd_qfused on checked arguments, with the key-split workspace when the plan needs
+    one (the device must be current)."""
+    ws, ws_ptr, ws_bytes = _split_workspace(True, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
+    _capi.call("sage_attn_i8_fwd_qfused", query.data_ptr(), key.data_ptr(), value_t.data_ptr(),
+               output.data_ptr(), lse.data_ptr() if lse is not None else _NULL, k_scale.data_ptr(),
+               _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, *qst, *ost, int(bool(is_causal)), float(sm_scale),
+               int(num_splits), ws_ptr, ws_bytes, stream)
+    del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
