@@ -1,4 +1,5 @@
-"""Build the gfx950 C-ABI library ``sageattention/libsage_mi355x.so`` in-tree.
+"""Build the gfx950 C-ABI library ``sageattention/libsage_mi355x.so`` and the compiled host layer of
+``sageattn`` (``sageattention/_sage_host.so``, linked against it) in-tree.
 
 Usage: ``python sageattention-rdna3_amd/build.py [-v]``.  Cross-compiles for
 gfx950 with hipcc; no GPU is needed.  Every call recompiles.
@@ -29,6 +30,11 @@ BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = os.environ.get("SAGE_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+GXX = os.environ.get("CXX", "g++")
+# the compiled host layer of sageattn (a Python extension module over the library's C ABI)
+HOST_MODULE = "_sage_host"
+HOST_SRC = "host_ops.cpp"
+HOST_PATH = os.path.join(OUT_DIR, HOST_MODULE + ".so")
 
 COMMON = [
     f"--offload-arch={ARCH}",
@@ -51,33 +57,67 @@ SOURCES = [
 ]
 
 
-def _run(cmd, verbose):
-    if verbose:
-        print(" ".join(shlex.quote(c) for c in cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    out = (res.stdout or "") + (res.stderr or "")
+def _finish(cmd, proc, verbose):
+    out, _ = proc.communicate()
     # hipcc's host pass does not know the device-only feature; that warning is expected
-    lines = [ln for ln in out.splitlines() if "packed-fp32-ops" not in ln]
-    if res.returncode != 0:
-        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n" + "\n".join(lines))
+    lines = [ln for ln in (out or "").splitlines() if "packed-fp32-ops" not in ln]
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n" + "\n".join(lines))
     if verbose and lines:
         print("\n".join(lines), flush=True)
 
 
+def _start(cmd, verbose):
+    if verbose:
+        print(" ".join(shlex.quote(c) for c in cmd), flush=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def _run(cmd, verbose):
+    _finish(cmd, _start(cmd, verbose), verbose)
+
+
+def _host_flags():
+    """g++ flags of the compiled host layer: torch's headers and libraries (the module uses the torch
+    C++ API for tensors and pybind11 for the Python call; no HIP code)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    inc = cpp_extension.include_paths() + [sysconfig.get_paths()["include"], INCLUDE]
+    libdir = cpp_extension.library_paths()[0]
+    compile_flags = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+                     f"-DTORCH_EXTENSION_NAME={HOST_MODULE}", *[f"-I{i}" for i in inc]]
+    link_flags = [f"-L{libdir}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", f"-Wl,-rpath,{libdir}",
+                  f"-L{OUT_DIR}", "-l:" + LIB_NAME, "-Wl,-rpath,$ORIGIN"]
+    return compile_flags, link_flags
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every source for gfx950 and link the shared library; returns its path."""
+    """Compile every source (the gfx950 library and the host module, in parallel), link the shared
+    library, then the host module against it; returns the library's path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    objs = []
+    jobs, objs = [], []
     for src, extra in SOURCES:
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
         cmd = [HIPCC, *COMMON, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
         if src.endswith(".cpp"):
             cmd[1:1] = ["-x", "hip"]
-        _run(cmd, verbose)
+        jobs.append((cmd, _start(cmd, verbose)))
         objs.append(obj)
+    host_cflags, host_lflags = _host_flags()
+    host_obj = os.path.join(BUILD_DIR, HOST_SRC.replace(".cpp", ".o"))
+    cmd = [GXX, *host_cflags, "-c", os.path.join(CSRC, HOST_SRC), "-o", host_obj]
+    jobs.append((cmd, _start(cmd, verbose)))
+    for cmd, proc in jobs:
+        _finish(cmd, proc, verbose)
     tmp = LIB_PATH + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{LIB_NAME}", *objs, "-o", tmp], verbose)
     os.replace(tmp, LIB_PATH)
+    tmp = HOST_PATH + ".tmp"
+    _run([GXX, "-shared", host_obj, "-o", tmp, *host_lflags], verbose)
+    os.replace(tmp, HOST_PATH)
     return LIB_PATH
 
 

@@ -20,13 +20,27 @@ import torch
 from . import _capi, ops
 
 
-def _vector_ready(t: torch.Tensor) -> torch.Tensor:
-    """Return ``t`` or a copy that satisfies the 16-byte access contract
-    (base aligned to 16 bytes, batch/head/token strides multiples of 8)."""
-    st = t.stride()
-    if t.data_ptr() % 16 == 0 and st[0] % 8 == 0 and st[1] % 8 == 0 and st[2] % 8 == 0:
-        return t
-    return t.contiguous() if not t.is_contiguous() else t.clone()
+_host_mod = None
+
+
+def _host():
+    """The compiled host layer (``_sage_host.so``, built beside the library); no fallback."""
+    global _host_mod
+    if _host_mod is None:
+        _capi.load()  # the library (and its ABI check) first; the module links against it
+        try:
+            from . import _sage_host
+        except ImportError as e:
+            raise RuntimeError(
+                "sageattention host module (_sage_host.so) is not available. Build it with:\n"
+                "  python sageattention-rdna3_amd/build.py\n"
+                f"Original error: {e}"
+            ) from e
+        if _sage_host.abi_version() != _capi.ABI_VERSION:
+            raise RuntimeError(f"_sage_host links ABI {_sage_host.abi_version()}, expected {_capi.ABI_VERSION}")
+        _sage_host.set_error_type(_capi.SageError)
+        _host_mod = _sage_host
+    return _host_mod
 
 
 def _env_int(name: str, default: int) -> int:
@@ -113,50 +127,20 @@ def sageattn(
     layout_code = ops.HND if tensor_layout == "HND" else ops.NHD
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k and v must be 4-D tensors")
-    q = _vector_ready(q)
-    k = _vector_ready(k)
-    v = _vector_ready(v)
-    (B, Hq, Sq, D), qst = ops._bhnd(q, layout_code)
-    (Bk, Hkv, Sk, Dk), kst = ops._bhnd(k, layout_code)
-    if tuple(k.shape) != tuple(v.shape) or Bk != B or Dk != D:
-        raise ValueError(f"incompatible shapes q={tuple(q.shape)} k={tuple(k.shape)} v={tuple(v.shape)}")
-    if Hq % Hkv != 0:
-        raise ValueError(f"number of query heads ({Hq}) must be a multiple of kv heads ({Hkv})")
-    vst = ops._bhnd(v, layout_code)[1]
-    o = torch.empty_like(q)
-    ost = ops._bhnd(o, layout_code)[1]
-    dev = q.device
+    seq = 2 if layout_code == ops.HND else 1
+    direct = use_direct_path(headdim, q.shape[seq], k.shape[seq], bool(is_causal), tensor_layout)
 
-    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=dev) if return_lse else None
-    num_splits = _env_int("SAGEATTN_KV_SPLITS", 0)
-
-    # the ops' launch helpers directly: the shapes, dtypes and layouts above already satisfy the
-    # checks the public ops make (and the library checks every launch again)
-    with ops._on_device(dev):
-        stream = ops._stream(q)
-        if use_direct_path(D, Sq, Sk, bool(is_causal), tensor_layout):
-            # V transform: fp16 V_T [B,Hkv,D,ceil64(Sk)] zero padded (core.py:145-152,171-180)
-            v_t = torch.empty(B, Hkv, D, (Sk + 63) // 64 * 64, device=dev, dtype=torch.float16)
-            ops._v_layout_launch(v, v_t, B, Hkv, Sk, D, vst, stream)
-            # direct kernel reads Q and K in place (core.py:141-164); K rows must not overlap
-            if kst[2] < D:
-                k = k.contiguous()
-                kst = ops._bhnd(k, layout_code)[1]
-            # fp16_attn_t / bf16_attn_t (core.py:153-164)
-            ops._direct_launch(q, k, v_t, o, lse, B, Hq, Hkv, Sq, Sk, D, qst, kst, ost, is_causal, sm_scale,
-                               num_splits, stream)
-        else:
-            smooth_k = kwargs.get("smooth_k", False)
-            k_mean = ops.mean_seq(k, layout_code) if smooth_k and Sk > 0 else None
-            # K quantisation and the V transform in one launch; Q is quantised inside the attention
-            # kernel (the same q_int8 and q_scale as quant_qk_int8 would produce, so the same output,
-            # without the int8 Q round trip)
-            k_int8, k_scale, v_t = ops._prep_kv_launch(k, v, k_mean, B, Hkv, Sk, D, kst, vst, stream)
-            # return_lse: the reference returns a zero placeholder (core.py:203-211); the fused kernel
-            # writes the real log-sum-exp of each row (natural log, scaled scores; -inf for a row
-            # without keys)
-            ops._qfused_launch(q, k_int8, v_t, o, lse, k_scale, B, Hq, Hkv, Sq, Sk, D, qst, ost, is_causal,
-                               sm_scale, num_splits, stream)
+    # the rest of the call (shapes, allocations, the launches of the direct or the INT8 path) in one
+    # compiled call over the C ABI (csrc/host_ops.cpp): direct = V transform + fp16_attn_t /
+    # bf16_attn_t (core.py:141-164); INT8 = [K mean] + K quantisation and V transform in one launch +
+    # the attention kernel that quantises Q itself (the q_int8 and q_scale of quant_qk_int8, so the same
+    # output).  return_lse: the reference returns a zero placeholder (core.py:203-211); both kernels
+    # write the real log-sum-exp of each row (natural log of the scaled scores; -inf without keys).
+    with ops._on_device(q.device):
+        res = _host().sageattn_fwd(q, k, v, layout_code, bool(is_causal), float(sm_scale), bool(return_lse),
+                                   bool(kwargs.get("smooth_k", False)), direct,
+                                   _env_int("SAGEATTN_KV_SPLITS", 0), ops._stream(q))
+    o, lse = res if return_lse else (res, None)
 
     if input_dtype == torch.float32:
         o = o.to(torch.float32)

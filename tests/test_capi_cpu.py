@@ -338,3 +338,27 @@ def test_package_surface():
 
     assert sageattention.__version__ == "0.1.0"
     assert set(sageattention.__all__) == {"sageattn", "sageattn_qk_int8_pv_fp16_cuda"}
+
+
+def test_host_module_loads_and_checks_shapes():
+    """The compiled host layer of sageattn loads, links the same ABI, and raises the Python side's
+    ValueErrors and SageError before any launch (CPU tensors; no kernel is reached)."""
+    from sageattention import core
+
+    host = core._host()
+    assert host.abi_version() == _capi.ABI_VERSION
+    q = torch.zeros(1, 4, 64, 64, dtype=torch.float16)
+    k3 = torch.zeros(1, 3, 64, 64, dtype=torch.float16)
+    args = (1, False, 0.125, False, False, True, 0, 0)
+    with pytest.raises(ValueError, match="4-D"):
+        host.sageattn_fwd(q[0], q, q, *args)
+    with pytest.raises(ValueError, match="multiple of kv heads"):
+        host.sageattn_fwd(q, k3, k3, *args)
+    with pytest.raises(ValueError, match="incompatible shapes"):
+        host.sageattn_fwd(q, q, q[:, :, :32], *args)
+    with pytest.raises(ValueError, match="num_splits"):
+        host.sageattn_fwd(q, q, q, 1, False, 0.125, False, False, True, 17, 0)
+    # head_dim 96: the library's V-layout entry rejects it before launching anything
+    q96 = torch.zeros(1, 4, 64, 96, dtype=torch.float16)
+    with pytest.raises(_capi.SageError, match="SAGE_ERR_UNSUPPORTED"):
+        host.sageattn_fwd(q96, q96, q96, *args)
