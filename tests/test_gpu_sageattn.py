@@ -243,3 +243,14 @@ class TestApiContract:
         q = randn(1, 2, 0, 64)
         k = randn(1, 2, 64, 64)
         assert sageattn(q, k, k).shape == q.shape
+
+    def test_empty_keys(self, sageattn):
+        # no key at all: every row's output is 0 and its log-sum-exp -inf (the oracle's convention)
+        q = randn(1, 2, 300, 128)
+        k = randn(1, 2, 0, 128)
+        o, lse = sageattn(q, k, k, return_lse=True)
+        assert o.shape == q.shape and not o.any()
+        assert lse.shape == (1, 2, 300) and bool(torch.all(lse == float("-inf")))
+        o, lse = sageattn(q.transpose(1, 2), k.transpose(1, 2), k.transpose(1, 2), tensor_layout="NHD",
+                          is_causal=True, return_lse=True, smooth_k=True)
+        assert not o.any() and bool(torch.all(lse == float("-inf")))
