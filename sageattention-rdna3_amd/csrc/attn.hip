@@ -257,6 +257,13 @@ __device__ __forceinline__ void wait_loads_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// The same, after the wave's LDS stores (and scalar loads) completed too, so
+// that what the waves wrote to LDS before it is visible to all after it.
+template <int N>
+__device__ __forceinline__ void wait_loads_lds_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // The tile's 4 key-group scales (INT8 path), read through the constant address
 // space so they land in SGPRs (the address is wave-uniform and nothing writes
 // the scales during the kernel); groups past the end repeat the last one and
@@ -826,7 +833,12 @@ __device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float
       if (lo + lane < hi) ks_a = ksp[lo + lane];
       if (lo + lane + 64 < hi) ks_b = ksp[lo + lane + 64];
     }
-    // fused kind: quantise Q while K_0, K_1, V_{-1} and the k scales are in flight
+    // K_2 and V_0 are the wave's last kStepLoads loads before the prologue
+    // barrier, which leaves them in flight (V_0 is waited for at step 1), so
+    // they are issued as early as the ring allows
+    tl.issue_k(rk, kring + 2 * C::kKStage, kv0 + 2 * kBN, wave);
+    tl.issue_v(rv, vring + 0 * C::kVStage, kv0, wave);
+    // fused kind: quantise Q while the tiles and the k scales are in flight
     if constexpr (QK == kQkI8F) qs = quant_q_raw<D, OUT_BF16>(p, wrow0, qraw, qf);
     if constexpr (is_i8(QK)) {
       float mx = __builtin_fmaxf(ks_a, ks_b);
@@ -835,7 +847,8 @@ __device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float
       for (int off = 32; off >= 1; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
       if (lane == 0) ks_part[wave] = mx;
     }
-    __syncthreads();  // K_0, K_1, V_{-1} landed; ks_part published
+    // K_0, K_1, V_{-1} landed (everything but K_2 and V_0); ks_part published
+    wait_loads_lds_barrier<C::kStepLoads>();
     bool fast_block = true;
     if constexpr (is_i8(QK)) {
       float kmax = 0.0f;
@@ -843,8 +856,6 @@ __device__ __forceinline__ void attn_item(const AttnParams& p, char* smem, float
       for (int w = 0; w < kWaves; ++w) kmax = __builtin_fmaxf(kmax, ks_part[w]);
       fast_block = qs * kmax < kFastScaleLimit;
     }
-    tl.issue_k(rk, kring + 2 * C::kKStage, kv0 + 2 * kBN, wave);
-    tl.issue_v(rv, vring + 0 * C::kVStage, kv0, wave);
     load_ks<QK>(p, ksp, kv0, ks);
     qk_tile<D, QK>(kread, om, qf, s, sinit);
 
