@@ -32,7 +32,10 @@ struct SageStatus {
   std::string msg;
 };
 
-py::object g_error_type;  // set by set_error_type(); RuntimeError until then
+// set by set_error_type(); RuntimeError until then.  A plain reference that is
+// never released: a py::object here would be decremented by a static
+// destructor after the interpreter has finalised.
+PyObject* g_error_type = nullptr;
 
 void check(const char* fn, int rc) {
   if (rc != SAGE_OK) {
@@ -175,7 +178,11 @@ py::object sageattn_fwd(at::Tensor q, at::Tensor k, at::Tensor v, int64_t layout
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "Compiled host layer of sageattn over the libsage_mi355x C ABI";
   m.def("abi_version", []() { return sage_abi_version(); });
-  m.def("set_error_type", [](py::object t) { g_error_type = std::move(t); });
+  m.def("set_error_type", [](py::object t) {
+    PyObject* old = g_error_type;
+    g_error_type = t.inc_ref().ptr();
+    Py_XDECREF(old);
+  });
   m.def("sageattn_fwd", &sageattn_fwd, py::arg("q"), py::arg("k"), py::arg("v"), py::arg("tensor_layout"),
         py::arg("is_causal"), py::arg("sm_scale"), py::arg("return_lse"), py::arg("smooth_k"), py::arg("direct"),
         py::arg("num_splits"), py::arg("stream"));
@@ -183,9 +190,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     try {
       if (p) std::rethrow_exception(p);
     } catch (const SageStatus& e) {
-      if (g_error_type && !g_error_type.is_none()) {
-        py::object err = g_error_type(e.fn, e.code, e.msg);
-        PyErr_SetObject(g_error_type.ptr(), err.ptr());
+      if (g_error_type != nullptr && g_error_type != Py_None) {
+        py::object type = py::reinterpret_borrow<py::object>(g_error_type);
+        py::object err = type(e.fn, e.code, e.msg);
+        PyErr_SetObject(g_error_type, err.ptr());
       } else {
         PyErr_SetString(PyExc_RuntimeError, (std::string(e.fn) + ": " + e.msg).c_str());
       }
