@@ -351,3 +351,39 @@ def _qfused_launch(query, key, value_t, output, lse, k_scale, B, Hq, Hkv, Sq, Sk
                _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, *qst, *ost, int(bool(is_causal)), float(sm_scale),
                int(num_splits), ws_ptr, ws_bytes, stream)
     del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
+
+
+# ---- torch.ops.sageattention: the reference's op namespace with its schemas (csrc/pybind_gfx11.cpp:18-47),
+# backed by the functions above (their extra keyword arguments keep their defaults), for callers that use the
+# op namespace directly.  Nothing is registered when the namespace is already taken (for instance by the
+# reference's own extension loaded into the same process).
+_SCHEMAS = {
+    "qk_int8_sv_bf16_attn_t": "qk_int8_sv_bf16_attn_t(Tensor query, Tensor key, Tensor value, Tensor(a!) output, "
+                              "Tensor q_scale, Tensor k_scale, int tensor_layout, int is_causal, float sm_scale"
+                              ") -> Tensor",
+    "fp16_attn_t": "fp16_attn_t(Tensor query, Tensor key, Tensor value, Tensor(a!) output, int tensor_layout, "
+                   "int is_causal, float sm_scale, int bm_sel) -> Tensor",
+    "bf16_attn_t": "bf16_attn_t(Tensor query, Tensor key, Tensor value, Tensor(a!) output, int tensor_layout, "
+                   "int is_causal, float sm_scale, int bm_sel) -> Tensor",
+    "quant_qk_int8": "quant_qk_int8(Tensor query, Tensor key, Tensor key_mean, int tensor_layout, float sm_scale"
+                     ") -> Tensor[]",
+    "mean_seq": "mean_seq(Tensor input, int tensor_layout) -> Tensor",
+    "v_transpose": "v_transpose(Tensor value, Tensor(a!) value_t, int tensor_layout) -> Tensor",
+}
+
+
+def _register_torch_ops():
+    try:
+        lib = torch.library.Library("sageattention", "DEF")
+    except RuntimeError:
+        return None
+    impls = {"qk_int8_sv_bf16_attn_t": qk_int8_sv_bf16_attn_t, "fp16_attn_t": fp16_attn_t,
+             "bf16_attn_t": bf16_attn_t, "quant_qk_int8": quant_qk_int8, "mean_seq": mean_seq,
+             "v_transpose": v_transpose}
+    for name, schema in _SCHEMAS.items():
+        lib.define(schema)
+        lib.impl(name, impls[name], "CUDA")
+    return lib
+
+
+_TORCH_LIBRARY = _register_torch_ops()

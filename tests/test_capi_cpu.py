@@ -362,3 +362,25 @@ def test_host_module_loads_and_checks_shapes():
     q96 = torch.zeros(1, 4, 64, 96, dtype=torch.float16)
     with pytest.raises(_capi.SageError, match="SAGE_ERR_UNSUPPORTED"):
         host.sageattn_fwd(q96, q96, q96, *args)
+
+
+def test_torch_ops_namespace_schemas():
+    """torch.ops.sageattention carries the reference's six ops with their schemas
+    (csrc/pybind_gfx11.cpp:18-38) and has no CPU kernel (the ops fail loudly off the GPU)."""
+    from sageattention import ops  # noqa: F401  (registers the namespace)
+
+    want = {
+        "qk_int8_sv_bf16_attn_t": "(Tensor query, Tensor key, Tensor value, Tensor(a!) output, Tensor q_scale, "
+                                  "Tensor k_scale, int tensor_layout, int is_causal, float sm_scale) -> Tensor",
+        "fp16_attn_t": "(Tensor query, Tensor key, Tensor value, Tensor(a!) output, int tensor_layout, "
+                       "int is_causal, float sm_scale, int bm_sel) -> Tensor",
+        "bf16_attn_t": "(Tensor query, Tensor key, Tensor value, Tensor(a!) output, int tensor_layout, "
+                       "int is_causal, float sm_scale, int bm_sel) -> Tensor",
+        "quant_qk_int8": "(Tensor query, Tensor key, Tensor key_mean, int tensor_layout, float sm_scale) -> Tensor[]",
+        "mean_seq": "(Tensor input, int tensor_layout) -> Tensor",
+        "v_transpose": "(Tensor value, Tensor(a!) value_t, int tensor_layout) -> Tensor",
+    }
+    for name, sig in want.items():
+        assert str(getattr(torch.ops.sageattention, name).default._schema) == f"sageattention::{name}{sig}"
+    with pytest.raises(NotImplementedError):
+        torch.ops.sageattention.mean_seq(torch.zeros(1, 2, 16, 64, dtype=torch.float16), 1)

@@ -287,6 +287,38 @@ def test_nondefault_stream_and_repeat_are_identical():
     assert torch.equal(o1, o2)
 
 
+def test_torch_ops_namespace_matches_ops():
+    """torch.ops.sageattention.* (the reference's op names and schemas) run the same kernels as the ops
+    module: identical bits, NHD layout, smooth_k, GQA."""
+    from sageattention import ops
+
+    cfg = Config("t", 1, 4, 2, 300, 64, "fp16", "NHD", False, True)
+    q, k, v = (t.cuda() for t in make_inputs(cfg, seed=7))
+    tops = torch.ops.sageattention
+    lay, sm = ops.NHD, 64 ** -0.5
+    mean = tops.mean_seq(k, lay)
+    assert torch.equal(mean, ops.mean_seq(k, lay))
+    got = tops.quant_qk_int8(q, k, mean, lay, sm)
+    want = ops.quant_qk_int8(q, k, mean, lay, sm)
+    assert len(got) == 4 and all(torch.equal(a, b) for a, b in zip(got, want))
+    q8, qs, k8, ks = got
+    vt = torch.empty(1, 2, 64, 320, device="cuda", dtype=torch.float16)
+    assert tops.v_transpose(v, vt, lay).data_ptr() == vt.data_ptr()
+    vt2 = torch.empty_like(vt)
+    assert torch.equal(vt, ops.v_transpose(v, vt2, lay))
+    o1, o2 = torch.empty_like(q), torch.empty_like(q)
+    tops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o1, qs, ks, lay, 0, sm)
+    ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o2, qs, ks, lay, 0, sm)
+    assert torch.equal(o1, o2)
+    for dt, name in ((torch.float16, "fp16_attn_t"), (torch.bfloat16, "bf16_attn_t")):
+        qd, kd = q.to(dt), k.to(dt)
+        o1, o2 = torch.empty_like(qd), torch.empty_like(qd)
+        getattr(tops, name)(qd, kd, vt, o1, lay, 1, sm, 0)
+        getattr(ops, name)(qd, kd, vt, o2, lay, 1, sm, 0)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and bool(torch.isfinite(o1.float()).all())
+
+
 # ------------------------------------------------------------------ LSE (this build's real return_lse)
 def gpu_attn_lse(cfg: Config, pro, dtype, q8=None, k8=None, vt=None, qs=None, ks=None):
     from sageattention import ops
