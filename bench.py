@@ -255,23 +255,27 @@ def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
             v = torch.randn((B, H, Sk, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
             direct = use_direct_path(D, Sq, Sk, False, "HND")
             calls = n if Sq * Sk >= 1 << 24 else max(n, 200)  # enough calls to time the short shapes
-            res = {}
-            for mode in modes:
-                if mode == "auto":
-                    os.environ.pop("SAGEATTN_KV_SPLITS", None)
-                else:
-                    os.environ["SAGEATTN_KV_SPLITS"] = mode
-                for _ in range(3):
-                    sageattn(q, k, v, tensor_layout="HND", is_causal=False)
-                torch.cuda.synchronize()
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                for _ in range(calls):
-                    sageattn(q, k, v, tensor_layout="HND", is_causal=False)
-                e1.record()
-                e1.synchronize()
-                res[mode] = e0.elapsed_time(e1) / calls
+            # the modes alternate over three rounds and each reports its median round, so that clock drift
+            # during the probe does not favour the mode measured first
+            times = {mode: [] for mode in modes}
+            for _round in range(3):
+                for mode in modes:
+                    if mode == "auto":
+                        os.environ.pop("SAGEATTN_KV_SPLITS", None)
+                    else:
+                        os.environ["SAGEATTN_KV_SPLITS"] = mode
+                    for _ in range(3):
+                        sageattn(q, k, v, tensor_layout="HND", is_causal=False)
+                    torch.cuda.synchronize()
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(calls):
+                        sageattn(q, k, v, tensor_layout="HND", is_causal=False)
+                    e1.record()
+                    e1.synchronize()
+                    times[mode].append(e0.elapsed_time(e1) / calls)
+            res = {mode: sorted(t)[1] for mode, t in times.items()}
             whole, splits = _capi.split_plan(not direct, B, H, Sq, Sk, D, False, 0)
             flops = attn_ops(B, H, Sq, Sk, D, False)
             row = {"shape": name, "B": B, "H": H, "Sq": Sq, "Sk": Sk, "D": D, "dtype": dt,
