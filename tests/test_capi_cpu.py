@@ -258,9 +258,10 @@ def test_prep_kv_zero_work_is_ok(lib):
 
 def test_split_workspace_bytes(lib):
     ws = lib.sage_attn_workspace_bytes
-    # forced counts: items (B*Hq*ceil(Sq/256)) x splits x 256 rows x (D + 1) fp32
+    # forced counts: items (B*Hq*ceil(Sq/256)) x splits x 256 rows x (D + 1) fp32; D = 64 non-causal
+    # launches run 128-row q-blocks (two blocks per CU): B*Hq*ceil(Sq/128) x splits x 128 rows
     assert ws(1, 1, 4, 64, 1024, 128, 0, 4) == 4 * 4 * 256 * 129 * 4
-    assert ws(0, 2, 3, 257, 5000, 64, 0, 16) == 2 * 3 * 2 * 16 * 256 * 65 * 4
+    assert ws(0, 2, 3, 257, 5000, 64, 0, 16) == 2 * 3 * 3 * 16 * 128 * 65 * 4
     assert ws(1, 1, 4, 64, 128, 128, 0, 4) == 4 * 2 * 256 * 129 * 4  # at most one split per 64 keys
     assert ws(1, 1, 4, 64, 1024, 128, 0, 1) == 0
     assert ws(1, 1, 4, 64, 1024, 128, 1, 4) == 0  # causal: never split
@@ -296,9 +297,10 @@ def test_automatic_plans_for_256_cus(lib):
     assert plan(True, 1, 32, 16384, 16384, 128, False, 0) == (2048, 1)   # 8 whole rounds
     assert plan(True, 1, 16, 4096, 4096, 128, False, 0) == (256, 1)      # exactly one round
     assert plan(True, 1, 3, 16384, 16384, 128, False, 0) == (192, 1)     # 192 q-blocks: estimated gain < 1.2x
-    assert plan(True, 1, 10, 9216, 9216, 64, False, 0) == (256, 2)       # 360 = 256 + 104
+    assert plan(True, 1, 10, 9216, 9216, 64, False, 0) == (720, 1)       # 720 128-row q-blocks: whole
     assert plan(True, 1, 3, 24576, 24576, 128, False, 0) == (256, 8)     # 288 = 256 + 32
-    assert plan(False, 1, 10, 2048, 2048, 64, False, 0) == (0, 3)        # 80 q-blocks
+    assert plan(False, 1, 10, 2048, 2048, 128, False, 0) == (0, 3)       # 80 q-blocks
+    assert plan(True, 1, 10, 4096, 4096, 64, False, 0) == (256, 4)       # 320 128-row q-blocks = 256 + 64
     assert plan(True, 2, 144, 256, 4096, 128, False, 0) == (256, 8)
     # a workspace-size query agrees with the plan: (q-blocks - whole) * splits * 256 rows * (D + 1) fp32
     assert lib.sage_attn_workspace_bytes(1, 1, 3, 24576, 24576, 128, 0, 0) == 32 * 8 * 256 * 129 * 4

@@ -160,12 +160,12 @@ def _with_env_splits(value, fn):
 
 
 def test_auto_split_of_a_small_grid():
-    """B1 H10 S2048 D64 fp16 (80 q-blocks for 256 CUs): the library's own plan splits every q-block,
+    """B1 H10 S2048 D128 fp16 (80 q-blocks for 256 CUs): the library's own plan splits every q-block,
     and sageattn's result (direct path) matches the unsplit one and the oracle."""
     from sageattention import _capi, sageattn
 
-    cfg = Config("small_grid", 1, 10, 10, 2048, 64, "fp16", "HND", False, False)
-    whole, n = _capi.split_plan(False, 1, 10, 2048, 2048, 64, False, 0)
+    cfg = Config("small_grid", 1, 10, 10, 2048, 128, "fp16", "HND", False, False)
+    whole, n = _capi.split_plan(False, 1, 10, 2048, 2048, 128, False, 0)
     _say(f"[auto split] plan: {whole} whole q-blocks, {n} splits")
     assert whole == 0 and n > 1
     q, k, v = make_inputs(cfg, seed=23)
@@ -176,10 +176,27 @@ def test_auto_split_of_a_small_grid():
     assert_close_to(cfg, o_auto, o_one)
     from sageattention import ops
 
-    vt = torch.empty(1, 10, 64, 2048, device="cuda", dtype=torch.float16)
+    vt = torch.empty(1, 10, 128, 2048, device="cuda", dtype=torch.float16)
     ops.v_transpose(vd, vt, ops.HND)
     rows = sample_rows(cfg.q_len, 64, np.random.default_rng(0))
     check_direct_rows(cfg, q, k, vt, o_auto, [0, 9], rows, cfg.D ** -0.5)
+
+
+def test_auto_tail_split_of_128_row_blocks():
+    """B1 H10 S4096 D64 fp16, INT8 path: 320 q-blocks of 128 rows (D = 64 non-causal runs two blocks
+    per CU); the plan runs 256 whole and splits the other 64; sageattn matches the unsplit launch."""
+    from sageattention import _capi, sageattn
+
+    cfg = Config("w4_tail", 1, 10, 10, 4096, 64, "fp16", "HND", False, False)
+    whole, n = _capi.split_plan(True, 1, 10, 4096, 4096, 64, False, 0)
+    _say(f"[128-row tail split] plan: {whole} whole q-blocks, {n} splits")
+    assert 0 < whole < 320 and n > 1
+    q, k, v = make_inputs(cfg, seed=29)
+    qd, kd, vd = (t.cuda() for t in (q, k, v))
+    o_auto = _with_env_splits(None, lambda: sageattn(qd, kd, vd, tensor_layout="HND", is_causal=False))
+    o_one = _with_env_splits("1", lambda: sageattn(qd, kd, vd, tensor_layout="HND", is_causal=False))
+    torch.cuda.synchronize()
+    assert_close_to(cfg, o_auto, o_one)
 
 
 def test_auto_tail_split_of_a_round_and_a_bit():
@@ -234,6 +251,8 @@ PERSISTENT = [
     Config("p_noncausal_gqa_h600", 1, 600, 150, 200, 128, "bf16", "NHD", False, False),
     Config("p_cross_causal_2x160", 2, 160, 40, 130, 64, "bf16", "HND", True, False, Sq=300),
     Config("p_smooth_b3", 3, 100, 100, 333, 128, "fp16", "HND", False, True),
+    # D = 64 non-causal runs 128-row q-blocks, two blocks per CU: 800 q-blocks over 512 slots
+    Config("p_noncausal_d64_h400", 1, 400, 400, 200, 64, "fp16", "HND", False, False),
 ]
 
 
