@@ -154,7 +154,9 @@ int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* val
 
 /*
  * Key splits of the two entry points below (non-causal launches only).  A
- * launch has B*Hq*ceil(q_len/256) blocks; when that leaves compute units idle
+ * launch has B*Hq*ceil(q_len/R) q-blocks, R = 128 query rows for head_dim 64
+ * (non-causal launches run two blocks per CU) and 256 otherwise (one block per
+ * CU); when that leaves compute units idle
  * (fewer blocks than CUs, or a last round partly filled) the key range of
  * some or all blocks can be split into parts whose fp32 partial outputs and
  * log-sum-exps a second launch merges exactly
@@ -180,8 +182,8 @@ int64_t sage_attn_workspace_bytes(int quantized, int64_t batch, int64_t q_heads,
                                   int64_t head_dim, int is_causal, int num_splits);
 
 /*
- * The split plan such a launch runs: q-blocks (256 query rows of one head,
- * numbered head-major) [0, *whole_qblocks) run whole, and every later one in
+ * The split plan such a launch runs: q-blocks (R query rows of one head as
+ * above, numbered head-major) [0, *whole_qblocks) run whole, and every later one in
  * *splits key ranges (*splits == 1: nothing is split).  num_splits 0 may
  * choose to split only the q-blocks of the last, partly filled round of the
  * device; a forced n > 1 splits every q-block.  Same arguments and

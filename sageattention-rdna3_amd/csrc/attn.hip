@@ -1,5 +1,9 @@
 // Fused flash attention for gfx950 (CDNA4, wave64 MFMA): the INT8 quantized
-// path and the direct fp16/bf16 path, one kernel template.
+// path and the direct fp16/bf16 path, one kernel template.  The kernels and
+// their host code live in attn_body.inc, compiled here in two block shapes;
+// this file holds the C entry points, which pick the shape per launch.  The
+// mapping below describes the 256-row shape (8 waves); the 128-row shape has
+// 4 waves and two blocks per CU.
 //
 // Math (csrc/attn_gfx11.cu of the reference):
 //   INT8   (:409-825)   s_ij = float(sum_d q8[i,d] * k8[j,d]) * (q_scale[i/32] * k_scale[j/16])
