@@ -81,6 +81,9 @@ SPLIT_CASES = [
     # 5 key tiles and 7 requested splits: one tile per split, the last one partial
     (Config("one_tile_per_split", 1, 2, 2, 300, 128, "fp16", "NHD", False, False), 7),
     (Config("d128_koffset_smooth", 1, 2, 2, 2049, 128, "bf16", "HND", False, True, k_offset_std=2.0), 4),
+    # D = 64 non-causal (128-row blocks of 4 waves): 9000 keys put more than 128 k-scale groups in each wave's
+    # share of the block's scale scan
+    (Config("d64_long_keys", 1, 2, 2, 9000, 64, "fp16", "HND", False, False, Sq=300), 2),
 ]
 
 
