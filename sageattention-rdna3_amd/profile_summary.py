@@ -1,7 +1,8 @@
 """Summaries of rocprofv3 output kept under profiles/ (text only).
 
-  python sageattention-rdna3_amd/profile_summary.py stats KERNEL_TRACE_CSV OUT_MD TITLE COMMAND
-      kernel trace -> markdown table of this library's kernels, one row per kernel and launch size
+  python sageattention-rdna3_amd/profile_summary.py stats KERNEL_TRACE_CSV OUT_MD TITLE COMMAND [LAST_N]
+      kernel trace -> markdown table of this library's kernels, one row per kernel and launch size (LAST_N:
+      also the average of each row's last LAST_N calls, bench.py's HIP-event loop)
   python sageattention-rdna3_amd/profile_summary.py traffic FETCH_CSV WRITE_CSV OUT_JSON OUT_MD COMMAND
       two --pmc runs of `bench.py --kernels-only` (FETCH_SIZE, then WRITE_SIZE) -> HBM bytes per
       launch of every path kernel, each counter scaled by what it reads for the 1 GiB device copy
@@ -46,9 +47,11 @@ def per_kernel(path, counter=None):
     return out
 
 
-def stats(trace_csv, out_md, title, command):
+def stats(trace_csv, out_md, title, command, last_n=0):
     """Per (kernel, grid) statistics from the kernel trace: one kernel runs at several shapes in one
-    bench.py run (the NS workload and the direct-path probe), and each shape gets its own row."""
+    bench.py run (the NS workload and the direct-path probe), and each shape gets its own row.  With
+    last_n, a column also averages each row's last last_n calls: for the path kernels of bench.py those
+    are its HIP-event loop (after the warm-up and the timed steps), the calls `roofline` times."""
     groups = collections.defaultdict(list)
     for r in csv.DictReader(open(trace_csv)):
         k = short_name(r["Kernel_Name"])
@@ -56,17 +59,25 @@ def stats(trace_csv, out_md, title, command):
             continue
         grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
         blocks = grid // max(1, int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"]))
-        groups[(k, blocks)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    total = sum(sum(v) for v in groups.values())
+        groups[(k, blocks)].append((int(r["Start_Timestamp"]),
+                                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    total = sum(sum(x for _, x in v) for v in groups.values())
+    last_n = int(last_n)
+    extra = f" avg of last {last_n} (us) |" if last_n else ""
     lines = [f"# {title}", "", "Command (repo root on the GPU box):", "", f"    {command}", "",
              "Calls include bench.py's warmup, timed steps and its per-kernel HIP-event loops; one row per kernel "
              "and launch size (workgroups).", "",
-             "| kernel | workgroups | calls | avg (us) | median (us) | min (us) | max (us) | share |",
-             "|---|---|---|---|---|---|---|---|"]
-    for (k, blocks), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+             "| kernel | workgroups | calls | avg (us) | median (us) | min (us) | max (us) | share |" + extra,
+             "|---|---|---|---|---|---|---|---|" + ("---|" if last_n else "")]
+    for (k, blocks), calls in sorted(groups.items(), key=lambda kv: -sum(x for _, x in kv[1])):
+        d = [x for _, x in sorted(calls)]
         med = sorted(d)[len(d) // 2]
-        lines.append(f"| `{k}` | {blocks} | {len(d)} | {sum(d) / len(d):.1f} | {med:.1f} | {min(d):.1f} | "
-                     f"{max(d):.1f} | {100 * sum(d) / total:.2f}% |")
+        row = (f"| `{k}` | {blocks} | {len(d)} | {sum(d) / len(d):.1f} | {med:.1f} | {min(d):.1f} | "
+               f"{max(d):.1f} | {100 * sum(d) / total:.2f}% |")
+        if last_n:
+            tail = d[-last_n:]
+            row += f" {sum(tail) / len(tail):.1f} |"
+        lines.append(row)
     open(out_md, "w").write("\n".join(lines) + "\n")
 
 
@@ -122,7 +133,7 @@ def counters(out_md, command, paths):
 if __name__ == "__main__":
     mode = sys.argv[1]
     if mode == "stats":
-        stats(*sys.argv[2:6])
+        stats(*sys.argv[2:7])
     elif mode == "traffic":
         traffic(*sys.argv[2:7])
     elif mode == "counters":
