@@ -1,0 +1,205 @@
+"""The product path itself -- ``sageattn`` and the fused-Q launch it makes -- at the BASELINE sizes, every
+output element written (NaN canaries), and the reference's own benchmark shapes in its NHD layout.
+
+* ``test_sageattn_full_size``: ``sageattn`` at NS, C3, C4 and C5 (what ``bench.py`` times: K mean when
+  smooth_k, K quantisation + V layout in one launch, the attention kernel that quantises Q itself, on the
+  persistent grid).  Its prologue inputs are checked bit-exact against the oracle, its output against the
+  oracle's rows (ends, tile and group boundaries, C5's ragged tail; the bars of test_gpu_parity), and against
+  the two-kernel ops path (quant_qk_int8 + qk_int8_sv_bf16_attn_t, reference core.py:165-198) bit for
+  bit whenever the launch runs unsplit (``SAGEATTN_KV_SPLITS=1`` forces that for a split plan).
+* NaN canaries: outputs and LSEs pre-filled with NaN through the ops API (ragged Sq, both layouts, both
+  block shapes, split and persistent plans, the direct kernel); no NaN may remain.  The reference shipped
+  this class of bug (NaN from unwritten V_T padding, NativeBackendOptimizeReport.md:183-196).
+* ``test_reference_shapes_nhd_accuracy``: the ten self-attention shapes of the reference's benchmark
+  (benchmark_attn/benchmark_attn.py:143-174) that its dispatch sends to the INT8 path, called as the
+  benchmark calls them (``[b, s, h, d]`` tensors, ``tensor_layout="NHD"``, :213-215,271) and held to its
+  FAIL threshold, max |out - sdpa| <= 0.05 (:216,310-317), and to cos >= 0.9999 (the band of
+  benchmark_attn-result-native.txt:4,22,25,43,46,64,70,73,79,82), on sampled rows of every head against
+  fp32 softmax attention cast to the output dtype, as the reference's get_sdpa_reference (:50-66).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sage_oracle as orc
+from _helpers import (BASELINE_CONFIGS, Config, cos_sim, make_inputs, np_to_f32, sample_rows,
+                      sdpa_rows_fp32, to_np)
+from test_gpu_parity import assert_prologue_exact, check_rows_vs_oracle, gpu_attn, gpu_prologue
+
+pytestmark = pytest.mark.gpu
+
+FULL = {c.name: c for c in BASELINE_CONFIGS}
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _lay(cfg):
+    from sageattention import ops
+
+    return ops.HND if cfg.layout == "HND" else ops.NHD
+
+
+def _sageattn(cfg, qd, kd, vd, splits=None):
+    from sageattention import sageattn
+
+    old = os.environ.get("SAGEATTN_KV_SPLITS")
+    if splits is not None:
+        os.environ["SAGEATTN_KV_SPLITS"] = str(splits)
+    try:
+        o = sageattn(qd, kd, vd, tensor_layout=cfg.layout, is_causal=cfg.causal, smooth_k=cfg.smooth_k)
+    finally:
+        if splits is not None:
+            if old is None:
+                os.environ.pop("SAGEATTN_KV_SPLITS", None)
+            else:
+                os.environ["SAGEATTN_KV_SPLITS"] = old
+    torch.cuda.synchronize()
+    return o
+
+
+def _plan(cfg):
+    from sageattention import _capi
+
+    return _capi.split_plan(1, cfg.B, cfg.Hq, cfg.q_len, cfg.S, cfg.D, int(cfg.causal), 0)
+
+
+@pytest.mark.parametrize("name", ["NS", "C3", "C4", "C5"])
+def test_sageattn_full_size(name):
+    from sageattention import ops
+    from sageattention.core import use_direct_path
+
+    cfg = FULL[name]
+    whole, splits = _plan(cfg)
+    _say(f"[sageattn full size] {cfg} plan=(whole {whole}, splits {splits})")
+    assert not use_direct_path(cfg.D, cfg.q_len, cfg.S, cfg.causal, cfg.layout)
+    q, k, v = make_inputs(cfg, seed=0)
+    qd, kd, vd = (t.cuda() for t in (q, k, v))
+    o = _sageattn(cfg, qd, kd, vd)
+
+    pro = gpu_prologue(cfg, q, k, v)
+    assert_prologue_exact(cfg, q, k, v, pro)
+    o_two = gpu_attn(cfg, pro, q.dtype)
+    if splits <= 1:
+        assert torch.equal(o, o_two), f"max diff {(o.float() - o_two.float()).abs().max().item()}"
+    else:
+        o1 = _sageattn(cfg, qd, kd, vd, splits=1)
+        assert torch.equal(o1, o_two), f"unsplit max diff {(o1.float() - o_two.float()).abs().max().item()}"
+
+    rng = np.random.default_rng(1)
+    rows = sample_rows(cfg.q_len, 40, rng)
+    heads = sorted({0, cfg.Hq - 1, int(rng.integers(0, cfg.Hq))})
+    worst = check_rows_vs_oracle(cfg, pro, o, heads, rows, cfg.dtype)
+
+    # the same launch through the ops layer into NaN-filled outputs: every element is written
+    lay = _lay(cfg)
+    k8, ks, vt = ops.prep_kv_int8(kd, vd, pro["mean"] if cfg.smooth_k else torch.empty(0, device="cuda",
+                                                                                        dtype=kd.dtype), lay)
+    o_nan = torch.full_like(qd, float("nan"))
+    lse = torch.full((cfg.B, cfg.Hq, cfg.q_len), float("nan"), device="cuda", dtype=torch.float32)
+    ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o_nan, ks, lay, int(cfg.causal), cfg.D ** -0.5, lse=lse)
+    torch.cuda.synchronize()
+    assert not bool(torch.isnan(o_nan).any()), "output element left unwritten"
+    assert bool(torch.isfinite(lse).all()), "LSE element left unwritten"
+    assert torch.equal(o_nan, o)
+    _say(f"  worst |gpu-oracle| = {worst:.3g}")
+
+
+# ------------------------------------------------------------------ NaN canaries
+CANARY = [
+    Config("ragged1000_d128_causal", 1, 4, 2, 1000, 128, "bf16", "HND", True, False),
+    Config("ragged300_d64_nhd", 2, 3, 3, 300, 64, "fp16", "NHD", False, False),
+    Config("ragged1000_d64_causal_nhd", 1, 4, 4, 1000, 64, "fp16", "NHD", True, False),
+    Config("ragged300_d128_nhd", 1, 6, 3, 300, 128, "bf16", "NHD", False, False),
+    Config("cross_q300_kv1000_d128", 1, 4, 4, 1000, 128, "fp16", "HND", False, False, Sq=300),
+    # 288 causal q-blocks of 256 rows: the persistent grid (more items than CUs)
+    Config("persistent_causal_d128", 1, 8, 8, 9000, 128, "bf16", "HND", True, False),
+    # 360 q-blocks of 128 rows (D = 64 non-causal): the library's tail-split plan
+    Config("tail_split_d64", 1, 20, 20, 2304, 64, "fp16", "NHD", False, False),
+]
+
+
+@pytest.mark.parametrize("cfg", CANARY, ids=lambda c: c.name)
+@pytest.mark.parametrize("splits", [0, 1, 3])
+def test_nan_canary_every_output_written(cfg, splits):
+    """o and lse start as NaN; the INT8 two-kernel op, the fused-Q op and the direct op must overwrite
+    every element (splits: 0 = the library's plan, 1 = unsplit, 3 = forced key splits; causal launches
+    ignore it)."""
+    from sageattention import ops
+
+    _say(f"[canary] {cfg} splits={splits}")
+    lay = _lay(cfg)
+    q, k, v = (t.cuda() for t in make_inputs(cfg, seed=11))
+    pro = gpu_prologue(cfg, q.cpu(), k.cpu(), v.cpu())
+    nan = float("nan")
+
+    def fresh():
+        return (torch.full_like(q, nan),
+                torch.full((cfg.B, cfg.Hq, cfg.q_len), nan, device="cuda", dtype=torch.float32))
+
+    results = {}
+    o, lse = fresh()
+    if splits == 1:
+        ops.qk_int8_sv_bf16_attn_t(pro["q8"], pro["k8"], pro["v_t"], o, pro["q_scale"], pro["k_scale"], lay,
+                                   int(cfg.causal), cfg.D ** -0.5, lse=lse)
+        results["two-kernel"] = (o, lse)
+    o, lse = fresh()
+    ops.qk_int8_sv_bf16_attn_qfused_t(q, pro["k8"], pro["v_t"], o, pro["k_scale"], lay, int(cfg.causal),
+                                      cfg.D ** -0.5, lse=lse, num_splits=splits)
+    results["fused-Q"] = (o, lse)
+    o, lse = fresh()
+    fn = ops.bf16_attn_t if cfg.dtype == "bf16" else ops.fp16_attn_t
+    fn(q, k, pro["v_t"], o, lay, int(cfg.causal), cfg.D ** -0.5, 0, lse=lse, num_splits=splits)
+    results["direct"] = (o, lse)
+    torch.cuda.synchronize()
+    for what, (o, lse) in results.items():
+        assert not bool(torch.isnan(o).any()), f"{what}: {int(torch.isnan(o).sum())} output elements unwritten"
+        assert bool(torch.isfinite(lse).all()), f"{what}: {int((~torch.isfinite(lse)).sum())} LSE elements unwritten"
+    if "two-kernel" in results:
+        assert torch.equal(results["two-kernel"][0], results["fused-Q"][0])
+
+
+# ------------------------------------------------------------------ the reference's benchmark shapes, NHD
+INT8_REFERENCE_SHAPES = [  # benchmark_attn/benchmark_attn.py:143-174 (name, b, h, s, d, dtype)
+    ("SDXL01", 1, 10, 4096, 64, "fp16"),
+    ("SDXLVAE01", 1, 4, 16384, 128, "fp16"),
+    ("SDXL07", 1, 10, 6144, 64, "fp16"),
+    ("SDXLVAE02", 1, 4, 24576, 128, "fp16"),
+    ("SDXL13", 1, 10, 9216, 64, "fp16"),
+    ("Anima01", 1, 16, 4096, 128, "bf16"),
+    ("AnimaVAE01", 1, 3, 16384, 128, "bf16"),
+    ("Anima03", 1, 16, 6144, 128, "bf16"),
+    ("AnimaVAE02", 1, 3, 24576, 128, "bf16"),
+    ("Anima05", 1, 16, 9216, 128, "bf16"),
+]
+
+
+@pytest.mark.parametrize("shape", INT8_REFERENCE_SHAPES, ids=lambda s: s[0])
+def test_reference_shapes_nhd_accuracy(shape):
+    from sageattention import sageattn
+    from sageattention.core import use_direct_path
+
+    name, B, H, S, D, dt = shape
+    cfg = Config(name, B, H, H, S, D, dt, "NHD", False, False)
+    assert not use_direct_path(D, S, S, False, "NHD"), "the reference's NHD dispatch sends this shape to INT8"
+    q, k, v = make_inputs(cfg, seed=0)
+    o = sageattn(q.cuda(), k.cuda(), v.cuda(), tensor_layout="NHD", is_causal=False)
+    torch.cuda.synchronize()
+    og = orc.to_hnd(np_to_f32(to_np(o), dt), "NHD")
+    qh, kh, vh = (orc.to_hnd(np_to_f32(to_np(t), dt), "NHD") for t in (q, k, v))
+    rows = sample_rows(S, 24, np.random.default_rng(2))
+    max_err, got_all, ref_all = 0.0, [], []
+    for h in range(H):
+        ref = sdpa_rows_fp32(qh[0, h], kh[0, h], vh[0, h], rows, False, D ** -0.5)
+        ref = np_to_f32(orc.from_f32(ref.astype(np.float32), dt), dt)  # get_sdpa_reference's .to(out_dtype)
+        got = og[0, h, rows]
+        max_err = max(max_err, float(np.max(np.abs(got.astype(np.float64) - ref))))
+        got_all.append(got)
+        ref_all.append(ref)
+    cs = cos_sim(np.concatenate(got_all), np.concatenate(ref_all))
+    _say(f"[reference shape NHD] {name}: MaxErr {max_err:.6f} CosSim {cs:.6f} ({len(rows)} rows x {H} heads)")
+    assert max_err <= 0.05, f"{name}: MaxErr {max_err} above the reference's FAIL threshold 0.05"
+    assert cs >= 0.9999, f"{name}: CosSim {cs}"
