@@ -10,11 +10,14 @@ TOPS of the whole step: 4*B*H*D*S(S+1)/2 / step time.
 ``roofline`` is that attention kernel alone, timed with HIP events on the
 stream it is launched on (torch's current stream): achieved = the same ops /
 average launch time, against the published dense INT8 MFMA peak of MI355X
-(5.0 POP/s).  ``cpu_baseline`` is the CPU oracle (numpy, all host cores its
-BLAS uses) on one head of the same workload, scaled to effective TOPS.
-``reference_shapes`` times whole ``sageattn`` calls at the reference's own
-benchmark shapes (non-causal SDXL / Anima / VAE lines), with and without the
-key splits the library plans for grids that leave CUs idle.
+(5.0 POP/s).  ``configs`` times the other BASELINE configs (C2-C5) the same way
+in the same run: the whole step, the attention kernel and the prologue kernels
+with their HBM fractions.  ``cpu_baseline`` is the PyTorch CPU implementation of
+the same quantized math (oracle/torch_cpu.py) on the host cores, on a fixed
+subset of heads scaled to the whole workload.  ``reference_shapes`` times whole
+``sageattn`` calls at the reference's own benchmark shapes, called as its
+benchmark calls them (NHD, non-causal), with MaxErr / MSE / CosSim against fp32
+attention as in its benchmark.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NS|C2|C3|C4|C5]
        python bench.py --reference-shapes all|NAME[,NAME...]
@@ -58,7 +61,13 @@ def attn_ops(B, H, Sq, Sk, D, causal):
     return 4 * B * H * D * pairs
 
 
-def make_inputs(cfg, device):
+# BASELINE.json input distributions beyond N(0,1): C3's per-channel K offset (std 2, shared across tokens) and
+# C5's x20 outlier channels (1% of D) in Q and K
+K_OFFSET_STD = {"C3": 2.0}
+OUTLIER_FRAC = {"C5": 0.01}
+
+
+def make_inputs(cfg, device, name=None):
     import torch
 
     B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
@@ -68,58 +77,65 @@ def make_inputs(cfg, device):
     def shp(h):
         return (B, h, S, D) if layout == "HND" else (B, S, h, D)
 
-    q = torch.randn(shp(Hq), generator=g, device=device, dtype=torch.float32).to(dtype)
-    k = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32).to(dtype)
-    v = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32).to(dtype)
-    return q, k, v
+    q = torch.randn(shp(Hq), generator=g, device=device, dtype=torch.float32)
+    k = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32)
+    v = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32)
+    if name in K_OFFSET_STD:
+        off = torch.randn((B, Hkv, 1, D), generator=g, device=device) * K_OFFSET_STD[name]
+        k += off if layout == "HND" else off.transpose(1, 2)
+    if name in OUTLIER_FRAC:
+        n_out = max(1, round(OUTLIER_FRAC[name] * D))
+        chans = torch.randperm(D, generator=g, device=device)[:n_out]
+        q[..., chans] *= 20.0
+        k[..., chans] *= 20.0
+    return q.to(dtype), k.to(dtype), v.to(dtype)
 
 
 def cpu_baseline(cfg, budget_s):
-    """Time the CPU oracle on one (b, h) head of the workload: quant + V layout +
-    attention of that head; returns the cpu_baseline object."""
-    import numpy as np
+    """The PyTorch CPU implementation of the same quantized math (oracle/torch_cpu.py: per-block INT8 Q/K
+    quantisation with fp32 scales, K mean for smooth_k, fp16 V, exact integer QK^T, fp32 online softmax over
+    key blocks with P rounded to fp16 before P.V), timed on the host cores: all of them
+    (torch.set_num_threads(len(os.sched_getaffinity(0)))), wall clock, 1 warm-up then the median of 3 runs,
+    on a fixed subset of query heads (as many as fit about a third of the time budget per run, at least one)
+    and scaled linearly by Hq.  Inputs are generated on the CPU from seed 0."""
+    import torch
 
     sys.path.insert(0, REPO)
-    from oracle import sage_oracle as orc
+    from oracle import torch_cpu
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        threads = len(os.sched_getaffinity(0))
     B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
-    rng = np.random.default_rng(0)
-    shp = (1, 1, S, D)
-    q, k, v = (orc.from_f32(rng.standard_normal(shp).astype(np.float32), dt) for _ in range(3))
-    t0 = time.perf_counter()
-    mean = orc.k_mean(k, dt, "HND") if smooth else None
-    q8, qs, k8, ks = orc.quant_qk_int8(q, k, dt, "HND", D ** -0.5, k_mean=mean)
-    vt = orc.v_layout(v, dt, "HND")
-    t_pro = time.perf_counter() - t0
-    # attention rows in 512-row blocks, from the last (heaviest for causal) down,
-    # until the whole head is done or the time budget is used
-    done_pairs, rows_done, t_attn = 0, 0, 0.0
-    for r1 in range(S, 0, -512):
-        rows = np.arange(max(0, r1 - 512), r1)
-        t1 = time.perf_counter()
-        orc.attn_i8_rows(q8, k8, vt, qs, ks, 0, 0, rows, causal)
-        t_attn += time.perf_counter() - t1
-        done_pairs += orc.pairs_for_rows(rows, S, causal)
-        rows_done += rows.size
-        if t_attn + t_pro > budget_s:
-            break
-    ops = 4 * D * done_pairs
-    # scale the prologue time to the rows done (it is computed for the whole head)
-    t_total = t_attn + t_pro * rows_done / S
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    dtype = torch.bfloat16 if dt == "bf16" else torch.float16
+    g = torch.Generator().manual_seed(0)
+    G = Hq // Hkv
+
+    def run(nh):
+        hk = max(1, -(-nh // G))
+        q = torch.randn((1, nh, S, D), generator=g).to(dtype)
+        k = torch.randn((1, hk, S, D), generator=g).to(dtype)
+        v = torch.randn((1, hk, S, D), generator=g).to(dtype)
+        t0 = time.perf_counter()
+        torch_cpu.sageattn_heads(q, k, v, causal, D ** -0.5, smooth_k=smooth)
+        return time.perf_counter() - t0
+
+    t_warm = run(1)  # warm-up (one head), also sizes the sample
+    nh = int(max(1, min(Hq, budget_s / 3.0 // max(t_warm, 1e-3))))
+    times = sorted(run(nh) for _ in range(3))
+    t_med = times[1]
+    ops = attn_ops(B, Hq, S, S, D, causal)
+    t_all = t_med * (B * Hq) / nh
+    info = torch.__config__.parallel_info().strip().splitlines()
     return {
-        "value": ops / t_total / 1e12,
+        "value": round(ops / t_all / 1e12, 5),
         "unit": "TOPS",
-        "cores": int(threads),
+        "cores": cores,
         "kind": "port",
-        "sample": (f"CPU oracle (numpy) on head 0 of 1x{Hq} heads: quant+V layout of the head "
-                   f"(pro-rated) + attention of {rows_done}/{S} query rows "
-                   f"({'causal ' if causal else ''}{done_pairs} key pairs), {t_total:.1f} s"),
+        "sample": (f"PyTorch CPU implementation of the quantized path (oracle/torch_cpu.py) on {nh} of {B * Hq} "
+                   f"query heads (all {S} rows, {'causal' if causal else 'non-causal'}), median of 3 runs after "
+                   f"1 warm-up: {t_med:.2f} s, scaled x{B * Hq / nh:.0f} to the workload"),
+        "threads": torch.get_num_threads(),
+        "parallel_info": [ln.strip() for ln in info if ln.strip()][:8],
     }
 
 
@@ -210,9 +226,10 @@ def direct_probe(dev, n):
 
 
 # the reference's own benchmark shapes (benchmark_attn/benchmark_attn.py:143-174, results in
-# benchmark_attn-result-native.txt; all non-causal HND, h_q == h_kv): name, B, H, Sq, Sk, D, dtype.  The
-# long self-attention shapes take the INT8 path, the short and cross-attention ones (kv 77, 154, 512,
-# self-attention up to 2304) the direct path, as the reference dispatches them.
+# benchmark_attn-result-native.txt; non-causal, h_q == h_kv, called with [b, s, h, d] tensors and
+# tensor_layout="NHD", :213-215,271): name, B, H, Sq, Sk, D, dtype.  The reference's NHD dispatch sends the
+# long self-attention shapes to the INT8 path and the short self-attention and cross-attention ones (kv 77,
+# 154, 512; self-attention up to 3072 at D = 64, 2048 at D = 128) to the direct path.
 REFERENCE_SHAPES = [
     ("SDXL01", 1, 10, 4096, 4096, 64, "fp16"), ("SDXL02", 1, 10, 4096, 77, 64, "fp16"),
     ("SDXL03", 1, 10, 4096, 154, 64, "fp16"), ("SDXL04", 1, 20, 1024, 1024, 64, "fp16"),
@@ -231,12 +248,36 @@ REFERENCE_SHAPES = [
 ]
 
 
+def fp32_reference_nhd(q, k, v):
+    """The reference benchmark's accuracy baseline (benchmark_attn.py:50-66): softmax attention in fp32 on
+    [b, s, h, d] inputs, cast to the output dtype.  Computed per head in row blocks from contiguous fp32
+    operands (plain matmuls, no half-precision batched products)."""
+    import torch
+
+    B, Sq, H, D = q.shape
+    out = torch.empty_like(q)
+    scale = D ** -0.5
+    for b in range(B):
+        for h in range(H):
+            kh = k[b, :, h].float().contiguous()
+            vh = v[b, :, h].float().contiguous()
+            kt = kh.t().contiguous()
+            for r0 in range(0, Sq, 4096):
+                qh = q[b, r0:r0 + 4096, h].float().contiguous()
+                p = torch.softmax((qh @ kt) * scale, dim=-1)
+                out[b, r0:r0 + 4096, h] = (p @ vh).to(q.dtype)
+    return out
+
+
 def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
-    """Whole ``sageattn`` calls (the reference's dispatch: quantisation, V layout and INT8 attention, or
-    V layout and the direct kernel) at the reference's benchmark shapes (``names``: a subset), back to
-    back on one stream, with the library's key-split plan and with splitting switched off
-    (SAGEATTN_KV_SPLITS=1).  ``ms`` is the time per call as a caller sees it: for the smallest
-    shapes the host's issue time per call, when it exceeds the GPU's."""
+    """Whole ``sageattn`` calls at the reference's benchmark shapes (``names``: a subset), called as its
+    benchmark calls them: [b, s, h, d] tensors, tensor_layout="NHD", non-causal, so the reference's NHD
+    dispatch picks the INT8 or the direct path.  Back to back on one stream, with the library's key-split
+    plan and with splitting switched off (SAGEATTN_KV_SPLITS=1), the two modes alternating over three rounds
+    (each reports its median round).  ``ms`` is the time per call as a caller sees it: for the smallest
+    shapes the host's issue time per call, when it exceeds the GPU's.  MaxErr, MSE and CosSim are the
+    reference benchmark's (benchmark_attn.py:50-66), over the whole output against fp32 attention cast to
+    the output dtype; ``status`` is its FAIL rule (MaxErr > 0.05)."""
     import torch
 
     from sageattention import _capi, sageattn
@@ -250,13 +291,11 @@ def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
                 continue
             dtype = torch.bfloat16 if dt == "bf16" else torch.float16
             g = torch.Generator(device=dev).manual_seed(0)
-            q = torch.randn((B, H, Sq, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-            k = torch.randn((B, H, Sk, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-            v = torch.randn((B, H, Sk, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-            direct = use_direct_path(D, Sq, Sk, False, "HND")
+            q = torch.randn((B, Sq, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            k = torch.randn((B, Sk, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            v = torch.randn((B, Sk, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            direct = use_direct_path(D, Sq, Sk, False, "NHD")
             calls = n if Sq * Sk >= 1 << 24 else max(n, 200)  # enough calls to time the short shapes
-            # the modes alternate over three rounds and each reports its median round, so that clock drift
-            # during the probe does not favour the mode measured first
             times = {mode: [] for mode in modes}
             for _round in range(3):
                 for mode in modes:
@@ -265,21 +304,29 @@ def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
                     else:
                         os.environ["SAGEATTN_KV_SPLITS"] = mode
                     for _ in range(3):
-                        sageattn(q, k, v, tensor_layout="HND", is_causal=False)
+                        sageattn(q, k, v, tensor_layout="NHD", is_causal=False)
                     torch.cuda.synchronize()
                     e0 = torch.cuda.Event(enable_timing=True)
                     e1 = torch.cuda.Event(enable_timing=True)
                     e0.record()
                     for _ in range(calls):
-                        sageattn(q, k, v, tensor_layout="HND", is_causal=False)
+                        sageattn(q, k, v, tensor_layout="NHD", is_causal=False)
                     e1.record()
                     e1.synchronize()
                     times[mode].append(e0.elapsed_time(e1) / calls)
             res = {mode: sorted(t)[1] for mode, t in times.items()}
+            os.environ.pop("SAGEATTN_KV_SPLITS", None)
+            o = sageattn(q, k, v, tensor_layout="NHD", is_causal=False).float()
+            ref = fp32_reference_nhd(q, k, v).float()
+            max_err = (o - ref).abs().max().item()
+            mse = ((o - ref) ** 2).mean().item()
+            cos = torch.nn.functional.cosine_similarity(o.flatten(), ref.flatten(), dim=0).item()
             whole, splits = _capi.split_plan(not direct, B, H, Sq, Sk, D, False, 0)
             flops = attn_ops(B, H, Sq, Sk, D, False)
-            row = {"shape": name, "B": B, "H": H, "Sq": Sq, "Sk": Sk, "D": D, "dtype": dt,
-                   "path": "direct" if direct else "int8", "plan": {"whole_qblocks": whole, "splits": splits}}
+            row = {"shape": name, "B": B, "H": H, "Sq": Sq, "Sk": Sk, "D": D, "dtype": dt, "layout": "NHD",
+                   "path": "direct" if direct else "int8", "plan": {"whole_qblocks": whole, "splits": splits},
+                   "max_err": round(max_err, 6), "mse": float(f"{mse:.3e}"), "cos": round(cos, 6),
+                   "status": "FAIL" if max_err > 0.05 else "OK"}
             if "auto" in res:
                 row.update(ms=round(res["auto"], 4), tops=round(flops / (res["auto"] * 1e-3) / 1e12, 1))
             if "1" in res:
@@ -287,14 +334,94 @@ def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
             out.append(row)
             log(f"[bench] {name} ({row['path']}): " +
                 ", ".join(f"{'sageattn' if m == 'auto' else 'unsplit'} {t:.4f} ms" for m, t in res.items()) +
-                f", plan {whole} whole + splits of {splits}")
-            del q, k, v
+                f", plan {whole} whole + splits of {splits}; MaxErr {max_err:.6f} CosSim {cos:.6f}")
+            del q, k, v, o, ref
     finally:
         if saved is None:
             os.environ.pop("SAGEATTN_KV_SPLITS", None)
         else:
             os.environ["SAGEATTN_KV_SPLITS"] = saved
     return out
+
+
+def config_probe(name, dev, n):
+    """One BASELINE config in the same run as the headline: the whole ``sageattn`` step, the attention kernel
+    alone (Q quantised in the kernel, what ``sageattn`` launches) against the INT8 peak, and the prologue
+    kernels (K quantisation + V layout in one launch, the K mean for smooth_k, the K-only quantisation)
+    against HBM, each on its own rotating input set so that no launch finds its operands in the caches."""
+    import torch
+
+    from sageattention import ops, sageattn
+
+    cfg = CONFIGS[name]
+    B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
+    q, k, v = make_inputs(cfg, dev, name)
+    lay = ops.HND if layout == "HND" else ops.NHD
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, calls):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        for _ in range(3):
+            fn()
+        e0.record(stream)
+        for _ in range(calls):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / calls
+
+    ms_step = timed(lambda: sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth), n)
+    mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=dev, dtype=q.dtype)
+    k8, ks, vt = ops.prep_kv_int8(k, v, mean, lay)
+    o = torch.empty_like(q)
+    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n)
+    NROT = 3
+    kr = [k] + [k.clone() for _ in range(NROT - 1)]
+    vr = [v] + [v.clone() for _ in range(NROT - 1)]
+    outs = [None] * NROT
+    rot = [0]
+
+    def rotated(fn):
+        def call():
+            i = rot[0] % NROT
+            rot[0] += 1
+            fn(i)
+        return call
+
+    ms_prep = timed(rotated(lambda i: outs.__setitem__(i, ops.prep_kv_int8(kr[i], vr[i], mean, lay))), n)
+    ms_kq = timed(rotated(lambda i: outs.__setitem__(i, ops.quant_k_int8(kr[i], mean, lay))), n)
+    ms_mean = timed(rotated(lambda i: ops.mean_seq(kr[i], lay)), n) if smooth else None
+    del kr, vr, outs
+    ops_step = attn_ops(B, Hq, S, S, D, causal)
+    nk = B * Hkv * S * D
+    kq_bytes = 2 * nk + nk + 4 * B * Hkv * ((S + 15) // 16)
+    vl_bytes = 2 * nk + 2 * B * Hkv * D * ((S + 63) // 64 * 64)
+    mean_bytes = 2 * nk + 2 * B * Hkv * D
+    ach = ops_step / (ms_attn * 1e-3) / 1e12
+    r = {
+        "workload": f"{name}: sageattn B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} {dt} {layout} "
+                    f"{'causal' if causal else 'non-causal'} smooth_k={smooth}",
+        "step_ms": round(ms_step, 5),
+        "effective_tops": round(ops_step / (ms_step * 1e-3) / 1e12, 2),
+        "attn_kernel_ms": round(ms_attn, 5),
+        "attn_frac_int8_peak": round(ach / PEAK_INT8_TOPS, 4),
+        "prep_kv_us": round(ms_prep * 1e3, 2),
+        "prep_kv_GBps": round((kq_bytes + vl_bytes) / ms_prep / 1e6, 1),
+        "prep_kv_frac_hbm": round((kq_bytes + vl_bytes) / ms_prep / 1e6 / PEAK_HBM_GBS, 4),
+        "k_quant_us": round(ms_kq * 1e3, 2),
+        "k_quant_GBps": round(kq_bytes / ms_kq / 1e6, 1),
+        "k_quant_frac_hbm": round(kq_bytes / ms_kq / 1e6 / PEAK_HBM_GBS, 4),
+        "k_mean_us": round(ms_mean * 1e3, 2) if smooth else None,
+        "k_mean_GBps": round(mean_bytes / ms_mean / 1e6, 1) if smooth else None,
+        "k_mean_frac_hbm": round(mean_bytes / ms_mean / 1e6 / PEAK_HBM_GBS, 4) if smooth else None,
+    }
+    log(f"[bench] {name}: step {ms_step:.4f} ms ({r['effective_tops']} TOPS), attention {ms_attn:.4f} ms "
+        f"({100 * r['attn_frac_int8_peak']:.1f}% INT8 peak), prep_kv {r['prep_kv_us']} us "
+        f"({100 * r['prep_kv_frac_hbm']:.1f}% HBM), K quant {r['k_quant_us']} us, K mean {r['k_mean_us']} us")
+    del q, k, v, o, k8, ks, vt
+    torch.cuda.empty_cache()
+    return r
 
 
 def main():
@@ -306,7 +433,10 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-probes", action="store_true",
-                    help="skip the direct-kernel and reference-shape probes (kernel traces of the NS workload alone)")
+                    help="skip the direct-kernel, reference-shape and per-config probes (kernel traces of the NS "
+                         "workload alone)")
+    ap.add_argument("--configs", default="C2,C3,C4,C5", metavar="NAMES",
+                    help="BASELINE configs timed after the headline (comma list, '' for none)")
     ap.add_argument("--reference-shapes", default=None, metavar="NAMES",
                     help="only time sageattn at these reference benchmark shapes (comma list, or 'all'), "
                          "print them as one JSON line and exit; for rocprofv3 runs of the split path")
@@ -347,7 +477,7 @@ def main():
               flush=True)
         return
 
-    q, k, v = make_inputs(cfg, dev)
+    q, k, v = make_inputs(cfg, dev, args.config)
     torch.cuda.synchronize()
     if args.kernels_only:
         kernels_only(cfg, q, k, v, args.steps)
@@ -437,7 +567,12 @@ def main():
         f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s; K quant + V layout in one launch "
         f"{ms_prep * 1e3:.1f} us = {(kquant_bytes + vl_bytes) / ms_prep / 1e6:.0f} GB/s")
 
+    del q8, qs, k8, ks, vt, o
+    torch.cuda.empty_cache()
     direct = None if args.no_probes else direct_probe(dev, n_k)
+    configs = None
+    if not args.no_probes and args.configs:
+        configs = {name: config_probe(name, dev, n_k) for name in args.configs.split(",") if name}
     ref_shapes = None if args.no_probes else reference_shapes_probe(dev, n_k)
 
     traffic = None
@@ -448,7 +583,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("[bench] CPU oracle baseline ...")
+        log("[bench] CPU baseline (PyTorch CPU implementation) ...")
         cpu = cpu_baseline(cfg, args.cpu_budget)
         log(f"[bench] cpu {cpu['value']:.4g} TOPS on {cpu['cores']} threads")
 
@@ -464,7 +599,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic N(0,1) inputs generated on the GPU from seed 0",
+        "data": "synthetic N(0,1) inputs generated on the GPU from seed 0 (C3: K plus a per-channel offset of std 2; "
+                "C5: 1% of the channels of Q and K x20)",
         "config": {
             "workload": f"{args.config}: sageattn B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} {dt} {layout} "
                         f"{'causal' if causal else 'non-causal'} smooth_k={smooth}",
@@ -499,6 +635,7 @@ def main():
             "k_mean_GBps": round(mean_bytes / ms_mean / 1e6, 1) if smooth else None,
         },
         "direct": direct,
+        "configs": configs,
         "reference_shapes": ref_shapes,
         "device": {"name": props.name, "cus": props.multi_processor_count},
         "cpu_baseline": cpu,

@@ -206,8 +206,12 @@ __global__ __launch_bounds__(256) void k_mean_partial_kernel(MeanParams p) {
 #pragma unroll
   for (int j = 0; j < PASSES; ++j) {
     const int row = row0 + j * SLOTS;
-    raw[j] = (row < p.s) ? *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(row) * p.sn)
-                         : make_uint4(0, 0, 0, 0);
+    raw[j] = make_uint4(0, 0, 0, 0);
+    if (row < p.s) {
+      // streaming: K is read again by the quantisation, but not by this launch
+      const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + static_cast<int64_t>(row) * p.sn));
+      raw[j] = make_uint4(t.x, t.y, t.z, t.w);
+    }
   }
   float acc[8];
 #pragma unroll
@@ -233,14 +237,25 @@ __global__ __launch_bounds__(256) void k_mean_partial_kernel(MeanParams p) {
   }
 }
 
-// Stage 2: one thread per (b, h, d) adds the chunk sums in chunk order.
+// Stage 2: one thread per (b, h, d) adds the chunk sums in chunk order.  The
+// loads of a batch of 16 chunk sums are all issued before the first add, so a
+// thread waits about one memory latency per 16 chunks rather than per chunk.
 template <bool BF16, int D>
 __global__ __launch_bounds__(D) void k_mean_final_kernel(MeanParams p) {
+  constexpr int kBatch = 16;
   const int t = threadIdx.x;
   const int64_t bh = blockIdx.x;
   const float* w = p.ws + bh * p.nchunks * D + t;
   float sum = 0.0f;
-  for (int c = 0; c < p.nchunks; ++c) sum = sum + w[static_cast<int64_t>(c) * D];
+  for (int c0 = 0; c0 < p.nchunks; c0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) v[i] = (c0 + i < p.nchunks) ? w[static_cast<int64_t>(c0 + i) * D] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (c0 + i < p.nchunks) sum = sum + v[i];
+    }
+  }
   const float m = sum / static_cast<float>(p.s);
   uint16_t out;
   if constexpr (BF16) {
@@ -274,8 +289,15 @@ __device__ __forceinline__ void v_layout_tile(const VLayoutParams& p, int64_t bl
   constexpr int LOADS = LOAD_TASKS / 256;
   constexpr int STORE_TASKS = D * (kVTile / 8);     // (channel, 8-token) tasks
   constexpr int STORES = STORE_TASKS / 256;
-  constexpr int LSTRIDE = PAIRS + 4;                // dwords per channel row (pad)
+  // tile[channel][pair]: 32 dwords per channel row, the pair index XORed with
+  // pswz(channel) (a multiple of 4, so each row's 16-byte groups stay whole
+  // for the ds_read_b128 of the store phase).  A load-phase write instruction
+  // covers channels 8cc + const of 16 chunks cc and 4 pairs: with pswz
+  // keyed on cc % 8 they land on 32 distinct banks (2-way; an unswizzled row
+  // pitch of 36 dwords put the 16 chunks on 2 banks, 8-way).
+  constexpr int LSTRIDE = PAIRS;
   __shared__ __align__(16) uint32_t tile[D * LSTRIDE];
+  auto pswz = [](int ch) { return ((ch >> 3) & 7) << 2; };
 
   const int t = threadIdx.x;
   const int64_t bh = blk / p.ntiles;
@@ -308,8 +330,9 @@ __device__ __forceinline__ void v_layout_tile(const VLayoutParams& p, int64_t bl
         lo = (wa[q] & 0xffffu) | (wc[q] << 16);
         hi = (wa[q] >> 16) | (wc[q] & 0xffff0000u);
       }
-      tile[(cc * 8 + 2 * q) * LSTRIDE + pr] = lo;
-      tile[(cc * 8 + 2 * q + 1) * LSTRIDE + pr] = hi;
+      const int c0 = cc * 8 + 2 * q, c1 = c0 + 1;
+      tile[c0 * LSTRIDE + (pr ^ pswz(c0))] = lo;
+      tile[c1 * LSTRIDE + (pr ^ pswz(c1))] = hi;
     }
   }
   __syncthreads();
@@ -319,12 +342,7 @@ __device__ __forceinline__ void v_layout_tile(const VLayoutParams& p, int64_t bl
     const int task = t + i * 256;
     const int n8 = task % (kVTile / 8);
     const int d = task / (kVTile / 8);
-    const uint32_t* s = &tile[d * LSTRIDE + n8 * 4];
-    uint4 w;
-    w.x = s[0];
-    w.y = s[1];
-    w.z = s[2];
-    w.w = s[3];
+    const uint4 w = *reinterpret_cast<const uint4*>(&tile[d * LSTRIDE + ((n8 * 4) ^ pswz(d))]);
     *reinterpret_cast<uint4*>(out + static_cast<int64_t>(d) * p.np + n8 * 8) = w;
   }
 }

@@ -184,6 +184,36 @@ def test_direct_validation(lib, kw, code, msg):
     assert msg in lib.sage_last_error().decode()
 
 
+@pytest.mark.parametrize("which", ["osb", "osh", "osn"])
+def test_negative_out_strides_are_rejected(lib, which):
+    for call in (attn, direct):
+        assert call(lib, **{which: -8}) == _capi.ERR_INVALID_ARG
+        assert "out strides must be non-negative" in lib.sage_last_error().decode()
+
+
+# The attention kernels address a head's K rows and V_T rows with 32-bit buffer offsets: the per-head
+# V_T span D * ceil64(Sk) * 2 bytes and the K span (Sk + 5 tiles) * k_stride_n * elem must stay within
+# UINT32_MAX.  Shapes one past either edge are refused before any launch.
+UINT32_MAX = 2 ** 32 - 1
+
+
+def test_32bit_limits_at_the_edge(lib):
+    # V_T: D = 128, np = 16777152 keeps 128 * np * 2 = 4294950912 <= UINT32_MAX; Sk one more pads to
+    # np = 16777216, i.e. 2^32 bytes
+    assert 128 * 16777152 * 2 <= UINT32_MAX < 128 * 16777216 * 2
+    for call in (attn, direct, qfused):
+        assert call(lib, Sk=16777153, causal=1) == _capi.ERR_UNSUPPORTED
+        assert "32-bit" in lib.sage_last_error().decode()
+    # K (direct kind, fp16, a strided K): (Sk + 320) * ksn * 2 bytes; Sk = 64, ksn one step (8) past
+    # the largest multiple of 8 that fits
+    ksn_max = UINT32_MAX // ((64 + 320) * 2) // 8 * 8
+    assert (64 + 320) * (ksn_max + 8) * 2 > UINT32_MAX >= (64 + 320) * ksn_max * 2
+    assert direct(lib, Sk=64, ksn=ksn_max + 8, ksh=ksn_max + 8, ksb=ksn_max + 8) == _capi.ERR_UNSUPPORTED
+    assert "32-bit" in lib.sage_last_error().decode()
+    # query lengths: q_len + one q-block must stay an int32
+    assert direct(lib, Sq=2 ** 31 - 256 + 1) == _capi.ERR_UNSUPPORTED
+
+
 def test_direct_zero_work_is_ok(lib):
     assert direct(lib, Sq=0) == _capi.OK
     assert direct(lib, B=0, q=NULL) == _capi.OK

@@ -507,3 +507,30 @@ def test_attn_ops_closed_form():
     assert orc.attn_ops(1, 32, 16384, 16384, 128, True) == 4 * 32 * 128 * (16384 * 16385 // 2)
     assert orc.attn_ops(1, 10, 4096, 4096, 64, False) == 4 * 10 * 64 * 4096 * 4096
     assert orc.pairs_for_rows(np.arange(10), 10, True) == 55
+
+
+# ------------------------------------------------------------------ the CPU baseline (oracle/torch_cpu.py)
+@pytest.mark.parametrize("cfg", [
+    Config("tc_bf16_causal", 1, 4, 2, 300, 128, "bf16", "HND", True, False),
+    Config("tc_fp16_ragged", 2, 3, 3, 97, 64, "fp16", "HND", False, False),
+], ids=lambda c: c.name)
+def test_torch_cpu_baseline_matches_oracle(cfg):
+    """bench.py's CPU baseline computes the same quantized math: its INT8 Q/K and scales equal the oracle's
+    bit for bit, and its attention rows (blockwise online softmax in fp32, small blocks so that several
+    key blocks and the causal diagonal are crossed) agree with the oracle's fp64 rows within the fp16
+    rounding of P (a running max that is not yet the row max rounds P at a different scale)."""
+    from oracle import torch_cpu as tc
+
+    q, k, v = make_inputs(cfg, seed=3)
+    sm = cfg.D ** -0.5
+    q8o, qso, k8o, kso = orc.quant_qk_int8(to_np(q), to_np(k), cfg.dtype, "HND", sm)
+    q8, qs, k8, ks, _ = tc.quant_qk(q, k, sm)
+    for got, want in ((q8, q8o), (qs, qso), (k8, k8o), (ks, kso)):
+        assert np.array_equal(got.numpy(), want)
+    vt = orc.v_layout(to_np(v), cfg.dtype, "HND")
+    out = tc.sageattn_heads(q, k, v, cfg.causal, sm, block=64)
+    rows = np.arange(cfg.S)
+    for h in range(cfg.Hq):
+        ref = orc.attn_i8_rows(q8o, k8o, vt, qso, kso, 0, h, rows, cfg.causal)
+        assert max_abs(out[h].numpy(), ref) < 1e-3
+        assert cos_sim(out[h].numpy(), ref) > 0.99999
