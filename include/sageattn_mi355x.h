@@ -216,6 +216,28 @@ int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* v
                             int64_t workspace_bytes, void* stream);
 
 /*
+ * sage_attn_i8_fwd_qfused without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The key
+ * splits' partial outputs go to a scratch array of 32 MiB that the library
+ * holds in each GPU's memory until the process ends; the call allocates
+ * nothing.  num_splits 0 picks the best plan whose partials fit the scratch;
+ * a forced n > 1 whose partials would not fit fails with SAGE_ERR_UNSUPPORTED.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (different streams, or host threads) race on it; calls ordered on one
+ * stream do not.  The first call that may split, per device, looks the
+ * scratch's address up (with that device current).  Results equal those of
+ * sage_attn_i8_fwd_qfused with the same num_splits.
+ */
+int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* k_i8, const void* value_t, void* out,
+                                    float* lse, const float* k_scale, int dtype,
+                                    int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                    int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                    int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                    int is_causal, double sm_scale, int num_splits, void* stream);
+
+/*
  * Direct attention without quantisation (the reference's short-sequence
  * branch): S = fp32(q . k) * fl(fl(sm_scale) * log2 e) from fp16/bf16 Q and K
  * (fp32 accumulation), the same masks and online softmax as sage_attn_i8_fwd,

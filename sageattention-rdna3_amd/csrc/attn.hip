@@ -122,7 +122,39 @@ bool small_blocks(int64_t head_dim, int is_causal) { return head_dim == 64 && is
 
 using namespace sage;
 
+// Scratch of sage_attn_i8_fwd_qfused_noalloc (the key splits' partial outputs
+// and LSEs): device memory the library holds until the process ends, one copy
+// per GPU.  The name is a host-side stand-in for host code; kernels get the
+// device address that hipGetSymbolAddress returns for the current device.
+constexpr int64_t kScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
 namespace {
+// The current device's address of `scratch`, looked up once per device (with
+// that device current) and kept; null with the error recorded if the runtime
+// cannot give it.
+void* scratch_address(const char* fn) {
+  constexpr int kDevs = 64;
+  static std::atomic<void*> cache[kDevs];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kDevs) {
+    (void)hipGetLastError();
+    set_error(SAGE_ERR_HIP, "%s: no current device (%s)", fn, e != hipSuccess ? hipGetErrorString(e) : "out of range");
+    return nullptr;
+  }
+  void* ptr = cache[dev].load(std::memory_order_acquire);
+  if (ptr != nullptr) return ptr;
+  e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    set_error(SAGE_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
+    return nullptr;
+  }
+  cache[dev].store(ptr, std::memory_order_release);
+  return ptr;
+}
+
 // attn_fwd of the block shape the launch runs (the arguments include head_dim and is_causal again)
 template <typename... Args>
 int run_attn(int64_t head_dim, int is_causal, Args... args) {
@@ -202,6 +234,38 @@ extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, co
                   q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
                   kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
                   is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_i8_fwd_qfused");
+}
+
+extern "C" int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* k_i8, const void* value_t, void* out,
+                                               float* lse, const float* k_scale, int dtype,
+                                               int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                               int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                               int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                               int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                               int is_causal, double sm_scale, int num_splits, void* stream) {
+  static const char* const fn = "sage_attn_i8_fwd_qfused_noalloc";
+  clear_error();
+  // a forced split count must fit the scratch (an automatic plan is chosen within it)
+  if (num_splits > 1 && is_causal == 0) {
+    int64_t whole = 0;
+    int splits = 0;
+    const int64_t need = split_plan(true, batch, q_heads, q_len, kv_len, head_dim, 0, num_splits, &whole, &splits);
+    if (need < 0) return static_cast<int>(need);
+    if (need > kScratchBytes)
+      return set_error(SAGE_ERR_UNSUPPORTED, "%s: %d key splits need %lld bytes of scratch, beyond its %lld", fn,
+                       num_splits, static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+  }
+  // only a launch that may split touches the scratch (causal launches, unsplit
+  // ones and empty ones never do)
+  void* ws = nullptr;
+  if (is_causal == 0 && num_splits != 1 && batch > 0 && q_len > 0 && kv_len > 0) {
+    ws = scratch_address(fn);
+    if (ws == nullptr) return SAGE_ERR_HIP;
+  }
+  return run_attn(head_dim, is_causal, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr, k_scale, dtype, batch,
+                  q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
+                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
+                  is_causal, sm_scale, num_splits, ws, ws != nullptr ? kScratchBytes : 0, stream, fn);
 }
 
 extern "C" int64_t sage_attn_workspace_bytes(int quantized, int64_t batch, int64_t q_heads, int64_t q_len,
