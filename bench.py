@@ -91,6 +91,42 @@ def make_inputs(cfg, device, name=None):
     return q.to(dtype), k.to(dtype), v.to(dtype)
 
 
+def queue_ahead(dev):
+    """Occupy the GPU for about 2 ms (a fill of 12 GiB, HBM-bound, not MFMA: a matmul here lowers the clock
+    for the next ~20 ms of MFMA work) so that the host can enqueue a whole timed loop while it runs: the
+    events then bracket back-to-back launches, not the host's per-call overhead, which at the shortest
+    kernels here (under 10 us) would otherwise be part of every launch's time."""
+    import torch
+
+    if dev not in _BUSY:
+        _BUSY[dev] = torch.empty(12 << 30, device=dev, dtype=torch.uint8)
+    _BUSY[dev].fill_(0)
+
+
+_BUSY = {}
+
+
+def timed_launches(fn, n, stream, dev, queue=True):
+    """Average time of one call of fn over n back-to-back calls, with HIP events on the launch stream (3 warm
+    calls first; with queue, the GPU kept busy while the n calls are enqueued -- for kernels shorter than the
+    host's per-call time)."""
+    import torch
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        fn()
+    if queue:
+        torch.cuda.synchronize(dev)
+        queue_ahead(dev)
+    e0.record(stream)
+    for _ in range(n):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
 def cpu_baseline(cfg, budget_s):
     """The PyTorch CPU implementation of the same quantized math (oracle/torch_cpu.py: per-block INT8 Q/K
     quantisation with fp32 scales, K mean for smooth_k, fp16 V, exact integer QK^T, fp32 online softmax over
@@ -193,7 +229,8 @@ def direct_probe(dev, n):
         e1.synchronize()
         return e0.elapsed_time(e1) / n
 
-    ms_kernel = timed(lambda: ops.bf16_attn_t(q, k, vt, o, lay, int(causal), D ** -0.5, 0))
+    ms_kernel = timed_launches(lambda: ops.bf16_attn_t(q, k, vt, o, lay, int(causal), D ** -0.5, 0), n, stream, dev,
+                               queue=False)
     ms_direct = timed(lambda: sageattn(q, k, v, tensor_layout=layout, is_causal=causal))
     names = ["SAGEATTN_DIRECT_THRESHOLD_D128", "SAGEATTN_DIRECT_THRESHOLD_D128_CROSS"]
     saved = {x: os.environ.get(x) for x in names}
@@ -348,7 +385,8 @@ def config_probe(name, dev, n):
     """One BASELINE config in the same run as the headline: the whole ``sageattn`` step, the attention kernel
     alone (Q quantised in the kernel, what ``sageattn`` launches) against the INT8 peak, and the prologue
     kernels (K quantisation + V layout in one launch, the K mean for smooth_k, the K-only quantisation)
-    against HBM, each on its own rotating input set so that no launch finds its operands in the caches."""
+    against HBM, each on its own rotating input set so that no launch finds its operands in the caches.
+    A device copy of prep_kv's byte count (half read, half written) gives the copy ceiling at that size."""
     import torch
 
     from sageattention import ops, sageattn
@@ -359,23 +397,16 @@ def config_probe(name, dev, n):
     lay = ops.HND if layout == "HND" else ops.NHD
     stream = torch.cuda.current_stream(dev)
 
-    def timed(fn, calls):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        for _ in range(3):
-            fn()
-        e0.record(stream)
-        for _ in range(calls):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / calls
+    def timed(fn, calls, queue=True):
+        return timed_launches(fn, calls, stream, dev, queue)
 
-    ms_step = timed(lambda: sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth), n)
+    ms_step = timed(lambda: sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth), n,
+                    queue=False)
     mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=dev, dtype=q.dtype)
     k8, ks, vt = ops.prep_kv_int8(k, v, mean, lay)
     o = torch.empty_like(q)
-    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n)
+    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n,
+                    queue=D < 128)
     NROT = 3
     kr = [k] + [k.clone() for _ in range(NROT - 1)]
     vr = [v] + [v.clone() for _ in range(NROT - 1)]
@@ -398,6 +429,12 @@ def config_probe(name, dev, n):
     kq_bytes = 2 * nk + nk + 4 * B * Hkv * ((S + 15) // 16)
     vl_bytes = 2 * nk + 2 * B * Hkv * D * ((S + 63) // 64 * 64)
     mean_bytes = 2 * nk + 2 * B * Hkv * D
+    # the copy ceiling at prep_kv's size: a device copy that reads and writes half of prep_kv's bytes each
+    half = (kq_bytes + vl_bytes) // 2 // 16 * 16
+    srcs = [torch.empty(half, device=dev, dtype=torch.uint8).fill_(1) for _ in range(NROT)]
+    dsts = [torch.empty_like(x) for x in srcs]
+    ms_copy = timed(rotated(lambda i: dsts[i].copy_(srcs[i])), n)
+    del srcs, dsts
     ach = ops_step / (ms_attn * 1e-3) / 1e12
     r = {
         "workload": f"{name}: sageattn B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} {dt} {layout} "
@@ -409,6 +446,9 @@ def config_probe(name, dev, n):
         "prep_kv_us": round(ms_prep * 1e3, 2),
         "prep_kv_GBps": round((kq_bytes + vl_bytes) / ms_prep / 1e6, 1),
         "prep_kv_frac_hbm": round((kq_bytes + vl_bytes) / ms_prep / 1e6 / PEAK_HBM_GBS, 4),
+        "copy_same_bytes_us": round(ms_copy * 1e3, 2),
+        "copy_same_bytes_GBps": round(2 * half / ms_copy / 1e6, 1),
+        "prep_kv_frac_of_copy": round(ms_copy / ms_prep, 4),
         "k_quant_us": round(ms_kq * 1e3, 2),
         "k_quant_GBps": round(kq_bytes / ms_kq / 1e6, 1),
         "k_quant_frac_hbm": round(kq_bytes / ms_kq / 1e6 / PEAK_HBM_GBS, 4),
@@ -418,7 +458,8 @@ def config_probe(name, dev, n):
     }
     log(f"[bench] {name}: step {ms_step:.4f} ms ({r['effective_tops']} TOPS), attention {ms_attn:.4f} ms "
         f"({100 * r['attn_frac_int8_peak']:.1f}% INT8 peak), prep_kv {r['prep_kv_us']} us "
-        f"({100 * r['prep_kv_frac_hbm']:.1f}% HBM), K quant {r['k_quant_us']} us, K mean {r['k_mean_us']} us")
+        f"({100 * r['prep_kv_frac_hbm']:.1f}% HBM; a copy of the same bytes {r['copy_same_bytes_us']} us = "
+        f"{r['copy_same_bytes_GBps']} GB/s), K quant {r['k_quant_us']} us, K mean {r['k_mean_us']} us")
     del q, k, v, o, k8, ks, vt
     torch.cuda.empty_cache()
     return r
@@ -437,6 +478,8 @@ def main():
                          "workload alone)")
     ap.add_argument("--configs", default="C2,C3,C4,C5", metavar="NAMES",
                     help="BASELINE configs timed after the headline (comma list, '' for none)")
+    ap.add_argument("--skip", default="", metavar="PROBES",
+                    help="comma list of probes to leave out: direct, reference (the reference benchmark shapes)")
     ap.add_argument("--reference-shapes", default=None, metavar="NAMES",
                     help="only time sageattn at these reference benchmark shapes (comma list, or 'all'), "
                          "print them as one JSON line and exit; for rocprofv3 runs of the split path")
@@ -510,22 +553,14 @@ def main():
     ops.v_transpose(v, vt, lay)
     o = torch.empty_like(q)
 
-    def timed(fn, n):
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        for _ in range(3):
-            fn()
-        e0.record(stream)
-        for _ in range(n):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / n
+    def timed(fn, n, queue=True):
+        return timed_launches(fn, n, stream, dev, queue)
 
     n_k = max(args.steps, 10)
-    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n_k)
+    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n_k,
+                    queue=False)
     ms_attn_unfused = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5),
-                            n_k)
+                            n_k, queue=False)
     # The prologue kernels stream HBM: back to back on the same tensors, part of their traffic would hit the
     # L2 / Infinity Cache (256 MB), so each launch gets its own input set out of NROT (together well past the
     # caches), and the output of a set is written while the next set is read.
@@ -569,11 +604,12 @@ def main():
 
     del q8, qs, k8, ks, vt, o
     torch.cuda.empty_cache()
-    direct = None if args.no_probes else direct_probe(dev, n_k)
+    skip = set(args.skip.split(",")) if args.skip else set()
+    direct = None if args.no_probes or "direct" in skip else direct_probe(dev, n_k)
     configs = None
     if not args.no_probes and args.configs:
         configs = {name: config_probe(name, dev, n_k) for name in args.configs.split(",") if name}
-    ref_shapes = None if args.no_probes else reference_shapes_probe(dev, n_k)
+    ref_shapes = None if args.no_probes or "reference" in skip else reference_shapes_probe(dev, n_k)
 
     traffic = None
     tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")

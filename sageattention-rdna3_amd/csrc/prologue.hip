@@ -314,8 +314,15 @@ __device__ __forceinline__ void v_layout_tile(const VLayoutParams& p, int64_t bl
     const int pr = task / CPR;
     const int n = n0 + 2 * pr;
     uint4 a = make_uint4(0, 0, 0, 0), c = make_uint4(0, 0, 0, 0);
-    if (n < p.s) a = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(n) * p.sn + cc * 8);
-    if (n + 1 < p.s) c = *reinterpret_cast<const uint4*>(base + static_cast<int64_t>(n + 1) * p.sn + cc * 8);
+    // streaming: each V byte is read once (non-temporal)
+    if (n < p.s) {
+      const u32x4_t t0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + static_cast<int64_t>(n) * p.sn + cc * 8));
+      a = make_uint4(t0.x, t0.y, t0.z, t0.w);
+    }
+    if (n + 1 < p.s) {
+      const u32x4_t t1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + static_cast<int64_t>(n + 1) * p.sn + cc * 8));
+      c = make_uint4(t1.x, t1.y, t1.z, t1.w);
+    }
     const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
     const uint32_t wc[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
