@@ -1,8 +1,10 @@
 """Build the gfx950 C-ABI library ``sageattention/libsage_mi355x.so`` and the compiled host layer of
 ``sageattn`` (``sageattention/_sage_host.so``, linked against it) in-tree.
 
-Usage: ``python sageattention-rdna3_amd/build.py [-v]``.  Cross-compiles for
-gfx950 with hipcc; no GPU is needed.  Every call recompiles.
+Usage: ``python sageattention-rdna3_amd/build.py [-v] [--asan]``.  Cross-compiles
+for gfx950 with hipcc; no GPU is needed.  Every call recompiles.  ``--asan``
+builds the host-AddressSanitizer variant of the library instead
+(``_build_asan/``, for the C-ABI tests on the CPU).
 
 Flags:
   * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` on every device
@@ -121,6 +123,46 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+# Host-side AddressSanitizer build of the C-ABI library: the same sources, with the host pass of every
+# compile instrumented (the device code is built as usual), for running the C-ABI validation tests under
+# ASan on the CPU.  Loaded through SAGEATTN_MI355X_LIB with the clang ASan runtime preloaded.
+ASAN_DIR = os.path.join(HERE, "_build_asan")
+ASAN_LIB = os.path.join(ASAN_DIR, "libsage_mi355x_asan.so")
+ASAN_HOST = ["-O1", "-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def asan_runtime() -> str:
+    """The clang ASan runtime that the instrumented library links against."""
+    out = subprocess.run([HIPCC, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    path = out.stdout.strip()
+    if not os.path.isabs(path) or not os.path.exists(path):
+        raise RuntimeError("clang ASan runtime (libclang_rt.asan-x86_64.so) not found")
+    return path
+
+
+def build_asan(verbose: bool = False) -> str:
+    """Build ASAN_LIB (host code instrumented); returns its path."""
+    os.makedirs(ASAN_DIR, exist_ok=True)
+    jobs, objs = [], []
+    common = [c for c in COMMON if c != "-O3"] + ASAN_HOST
+    for src, extra in SOURCES:
+        obj = os.path.join(ASAN_DIR, os.path.splitext(src)[0] + ".o")
+        cmd = [HIPCC, *common, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+        if src.endswith(".cpp"):
+            cmd[1:1] = ["-x", "hip"]
+        jobs.append((cmd, _start(cmd, verbose)))
+        objs.append(obj)
+    for cmd, proc in jobs:
+        _finish(cmd, proc, verbose)
+    tmp = ASAN_LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address", "-shared-libsan",
+          *objs, "-o", tmp], verbose)
+    os.replace(tmp, ASAN_LIB)
+    return ASAN_LIB
+
+
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
-    print(path)
+    if "--asan" in sys.argv:
+        print(build_asan(verbose="-v" in sys.argv))
+    else:
+        print(build(verbose="-v" in sys.argv))
