@@ -176,8 +176,8 @@ def cpu_baseline(cfg, budget_s):
 
 
 def kernels_only(cfg, q, k, v, n):
-    """Each kernel of the path n times, then a plain copy of 1 GiB n times (a
-    kernel of known traffic: FETCH_SIZE and WRITE_SIZE should read 1 GiB each)."""
+    """Each kernel of the path n times, the direct kernel at DIRECT_CFG n times, then a plain copy of 1 GiB n
+    times (a kernel of known traffic: FETCH_SIZE and WRITE_SIZE should read 1 GiB each)."""
     import torch
 
     from sageattention import ops
@@ -189,6 +189,14 @@ def kernels_only(cfg, q, k, v, n):
         k8, ks, vt = ops.prep_kv_int8(k, v, mean, lay)
         o = torch.empty_like(q)
         ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5)
+    dq, dk, dv = make_inputs(DIRECT_CFG, q.device)
+    dB, dH, _, dS, dD = DIRECT_CFG[:5]
+    dvt = torch.empty(dB, dH, dD, (dS + 63) // 64 * 64, device=q.device, dtype=torch.float16)
+    ops.v_transpose(dv, dvt, ops.HND)
+    do = torch.empty_like(dq)
+    for _ in range(n):
+        ops.bf16_attn_t(dq, dk, dvt, do, ops.HND, int(DIRECT_CFG[7]), dD ** -0.5, 0)
+    del dq, dk, dv, dvt, do
     src = torch.empty(1 << 30, dtype=torch.uint8, device=q.device)
     dst = torch.empty_like(src)
     for _ in range(n):
@@ -486,7 +494,7 @@ def main():
     ap.add_argument("--reference-modes", default="auto,1", metavar="MODES",
                     help="with --reference-shapes: 'auto' (the library's key-split plan) and/or '1' (unsplit)")
     ap.add_argument("--kernels-only", action="store_true",
-                    help="launch each path kernel --steps times plus a 1 GiB device copy (the HBM-counter "
+                    help="launch each path kernel and the direct kernel --steps times plus a 1 GiB device copy (the HBM-counter "
                          "calibration) and exit; for rocprofv3 --pmc runs")
     args = ap.parse_args()
 

@@ -113,19 +113,62 @@ def traffic(fetch_csv, write_csv, out_json, out_md, command):
     open(out_md, "w").write("\n".join(lines) + "\n")
 
 
-def counters(out_md, command, paths):
+def dispatch_facts(path):
+    """{kernel: {"duration_us": mean, "scratch": .., "LDS": ..}} of a counter CSV."""
+    dur = collections.defaultdict(dict)
+    res = collections.defaultdict(dict)
+    for r in csv.DictReader(open(path)):
+        k = short_name(r["Kernel_Name"])
+        if k is None:
+            continue
+        dur[k][r["Dispatch_Id"]] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        res[k].update(scratch=int(r["Scratch_Size"]), LDS=int(r["LDS_Block_Size"]))
+    for k, d in dur.items():
+        res[k]["duration_us"] = sum(d.values()) / len(d)
+    return res
+
+
+def counters(out_md, command, paths, xcds=8, simds=1024):
+    """Mean of every counter per kernel over the runs' dispatches, with derived figures: the kernel's cycles
+    (GRBM_GUI_ACTIVE counts each XCD's clocks, summed over the XCDs), the MFMA pipe's busy share of every
+    SIMD's cycles, and instructions per MFMA.  The dispatch time under the profiler includes the counter
+    set-up, so cycles over it understate the clock; use a kernel trace's duration for that."""
     merged = collections.defaultdict(dict)
+    facts = collections.defaultdict(dict)
     for pth in paths:
         for k, cs in per_kernel(pth).items():
             for c, vals in cs.items():
                 merged[k][c] = sum(vals) / len(vals)
+        for k, f in dispatch_facts(pth).items():
+            facts[k].setdefault("durations", []).append(f.pop("duration_us"))
+            facts[k].update(f)
     lines = ["# rocprofv3 --pmc counters per kernel (mean over dispatches, summed over dimensions)", "",
              "Commands (repo root on the GPU box), one counter group per run:", ""]
     lines += [f"    {c}" for c in command.split(" ;; ")]
-    lines += [""]
+    lines += ["", f"Derived: cycles = GRBM_GUI_ACTIVE / {xcds} XCDs; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / {simds} SIMDs / "
+              "cycles; per-MFMA ratios divide by SQ_INSTS_MFMA.  The dispatch time under the profiler includes the "
+              "counter set-up: a kernel trace gives the kernel's own duration.", ""]
     for k in sorted(merged):
-        lines += [f"## `{k}`", "", "| counter | value |", "|---|---|"]
-        lines += [f"| {c} | {v:.4g} |" for c, v in sorted(merged[k].items())]
+        c = merged[k]
+        f = facts.get(k, {})
+        lines += [f"## `{k}`", ""]
+        if f:
+            t = sum(f["durations"]) / len(f["durations"])
+            lines += [f"Dispatch: {t:.1f} us under the profiler; scratch {f['scratch']} B, LDS {f['LDS']} B.", ""]
+            derived = []
+            if "GRBM_GUI_ACTIVE" in c:
+                cyc = c["GRBM_GUI_ACTIVE"] / xcds
+                derived.append(f"{cyc:.4g} cycles")
+                if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                    derived.append(f"MFMA busy {c['SQ_VALU_MFMA_BUSY_CYCLES'] / simds / cyc:.1%} of each SIMD's cycles")
+            if c.get("SQ_INSTS_MFMA"):
+                for name in ("SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_LDS"):
+                    if name in c:
+                        derived.append(f"{name} per MFMA {c[name] / c['SQ_INSTS_MFMA']:.2f}")
+            if derived:
+                lines += ["Derived: " + "; ".join(derived) + ".", ""]
+        lines += ["| counter | value |", "|---|---|"]
+        lines += [f"| {n} | {v:.4g} |" for n, v in sorted(c.items())]
         lines += [""]
     open(out_md, "w").write("\n".join(lines) + "\n")
 
