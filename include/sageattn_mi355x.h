@@ -216,6 +216,29 @@ int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* v
                             int64_t workspace_bytes, void* stream);
 
 /*
+ * sage_attn_i8_fwd_qfused for fp16 inputs with V read in place: `value` is
+ * the caller's fp16 V [B,Hkv,Sk,D] through its strides (HND or NHD; 16-byte
+ * aligned base, strides multiples of 8 elements, rows not overlapping) instead
+ * of a V_T from sage_v_layout, so the V layout pass and its HBM round trip
+ * are skipped (the kernel transposes V tiles in LDS with ds_read_b64_tr_b16).
+ * dtype must be SAGE_DTYPE_F16 (Q, V and out); K from sage_quant_qk_i8 as for
+ * sage_attn_i8_fwd_qfused.  The MFMAs see the same V values in the same
+ * order, so results equal sage_v_layout + sage_attn_i8_fwd_qfused bit for
+ * bit.  No single reference counterpart: it replaces v_transpose
+ * (csrc/attn_gfx11.cu:1889-1935, kernel :323-407; sageattention/core.py:173-179)
+ * followed by the INT8 attention (:2069-2273) for fp16 V.
+ */
+int sage_attn_i8_fwd_qfused_vrows(const void* query, const int8_t* k_i8, const void* value, void* out,
+                                  float* lse, const float* k_scale, int dtype,
+                                  int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                  int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                  int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                  int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n,
+                                  int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                  int is_causal, double sm_scale, int num_splits, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
+/*
  * sage_attn_i8_fwd_qfused without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The key

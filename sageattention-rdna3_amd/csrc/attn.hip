@@ -189,7 +189,7 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
   clear_error();
   return run_attn(head_dim, is_causal, w8::kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale, k_scale, out_dtype,
                   batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim,
-                  head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h,
+                  head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h,
                   o_stride_n, is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd");
 }
 
@@ -202,7 +202,7 @@ extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, cons
   clear_error();
   return run_attn(head_dim, is_causal, w8::kQkI8, q_i8, k_i8, value_t, out, lse, q_scale, k_scale, out_dtype, batch,
                   q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim, head_dim,
-                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
+                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
                   is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd_lse");
 }
 
@@ -217,7 +217,7 @@ extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const vo
   clear_error();
   return run_attn(head_dim, is_causal, dtype == SAGE_DTYPE_BF16 ? w8::kQkBf16 : w8::kQkF16, query, key, value_t,
                   out, lse, nullptr, nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b,
-                  q_stride_h, q_stride_n, k_stride_b, k_stride_h, k_stride_n, o_stride_b, o_stride_h, o_stride_n,
+                  q_stride_h, q_stride_n, k_stride_b, k_stride_h, k_stride_n, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
                   is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_direct_fwd");
 }
 
@@ -232,8 +232,25 @@ extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, co
   clear_error();
   return run_attn(head_dim, is_causal, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr, k_scale, dtype, batch,
                   q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
-                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
+                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
                   is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_i8_fwd_qfused");
+}
+
+extern "C" int sage_attn_i8_fwd_qfused_vrows(const void* query, const int8_t* k_i8, const void* value, void* out,
+                                             float* lse, const float* k_scale, int dtype,
+                                             int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                             int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                             int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                             int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n,
+                                             int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                             int is_causal, double sm_scale, int num_splits, void* workspace,
+                                             int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return run_attn(head_dim, is_causal, w8::kQkI8FV, query, k_i8, value, out, lse, nullptr, k_scale, dtype, batch,
+                  q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
+                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, v_stride_b, v_stride_h, v_stride_n,
+                  o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes,
+                  stream, "sage_attn_i8_fwd_qfused_vrows");
 }
 
 extern "C" int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* k_i8, const void* value_t, void* out,
@@ -264,7 +281,7 @@ extern "C" int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* 
   }
   return run_attn(head_dim, is_causal, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr, k_scale, dtype, batch,
                   q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
-                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, o_stride_b, o_stride_h, o_stride_n,
+                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
                   is_causal, sm_scale, num_splits, ws, ws != nullptr ? kScratchBytes : 0, stream, fn);
 }
 

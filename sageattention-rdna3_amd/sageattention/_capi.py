@@ -62,6 +62,10 @@ SIGNATURES = {
                                      _I64, _I64, _I64, _I64, _I64, _I64,
                                      _I64, _I64, _I64, _I64, _I64, _I64,
                                      _I, ctypes.c_double, _I, _P, _I64, _P]),
+    "sage_attn_i8_fwd_qfused_vrows": (_I, [_P, _P, _P, _P, _P, _P, _I,
+                                           _I64, _I64, _I64, _I64, _I64, _I64,
+                                           _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                           _I, ctypes.c_double, _I, _P, _I64, _P]),
     "sage_attn_i8_fwd_qfused_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I,
                                              _I64, _I64, _I64, _I64, _I64, _I64,
                                              _I64, _I64, _I64, _I64, _I64, _I64,

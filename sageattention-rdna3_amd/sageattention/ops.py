@@ -353,6 +353,46 @@ def _qfused_launch(query, key, value_t, output, lse, k_scale, B, Hq, Hkv, Sq, Sk
     del ws  # stream-ordered: the caching allocator hands it out again only behind this launch
 
 
+def qk_int8_sv_f16_attn_qfused_vrows(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                     output: torch.Tensor, k_scale: torch.Tensor, tensor_layout: int,
+                                     is_causal: int, sm_scale: float,
+                                     lse: Optional[torch.Tensor] = None, num_splits: int = 0) -> torch.Tensor:
+    """:func:`qk_int8_sv_bf16_attn_qfused_t` for fp16 inputs with ``value`` the caller's fp16 V itself
+    (``[B, Hkv, Sk, D]`` in ``tensor_layout``, read through its strides) instead of a V_T from
+    :func:`v_transpose`: the kernel transposes V tiles in LDS, so the V layout pass is skipped.  Same
+    result bit for bit as ``v_transpose`` followed by :func:`qk_int8_sv_bf16_attn_qfused_t`.  This build's
+    fusion; it replaces the reference's v_transpose + INT8 attention pair (core.py:173-179,190-197) for
+    fp16 V."""
+    (B, Hq, Sq, D), qst = _bhnd(query, tensor_layout)
+    if query.dtype != torch.float16 or output.dtype != torch.float16 or value.dtype != torch.float16:
+        raise ValueError("query, value and output must be fp16 (V is read as fp16 in place)")
+    if query.stride(-1) != 1:
+        raise ValueError("query needs a contiguous head_dim axis")
+    Bk, Hkv, Sk, Dk = key.shape
+    if Bk != B or Dk != D or key.dtype != torch.int8 or not key.is_contiguous():
+        raise ValueError("key must be contiguous int8 [B,Hkv,Sk,D]")
+    (Bv, Hv, Sv, Dv), vst = _bhnd(value, tensor_layout)
+    if (Bv, Hv, Sv, Dv) != (B, Hkv, Sk, D) or value.stride(-1) != 1:
+        raise ValueError(f"value must be fp16 [{B},{Hkv},{Sk},{D}] in the tensor layout with a contiguous head_dim")
+    if (tuple(k_scale.shape) != (B, Hkv, (Sk + 15) // 16) or k_scale.dtype != torch.float32
+            or not k_scale.is_contiguous()):
+        raise ValueError("k_scale must be contiguous fp32 [B,Hkv,ceil(Sk/16)]")
+    (Bo, Ho, So, Do), ost = _bhnd(output, tensor_layout)
+    if (Bo, Ho, So, Do) != (B, Hq, Sq, D) or output.stride(-1) != 1:
+        raise ValueError("output shape does not match the query")
+    if lse is not None:
+        if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+            raise ValueError(f"lse must be contiguous fp32 [{B},{Hq},{Sq}]")
+    with _on_device(query.device):
+        ws, ws_ptr, ws_bytes = _split_workspace(True, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
+        _capi.call("sage_attn_i8_fwd_qfused_vrows", query.data_ptr(), key.data_ptr(), value.data_ptr(),
+                   output.data_ptr(), lse.data_ptr() if lse is not None else _NULL, k_scale.data_ptr(),
+                   _dtype_code(query), B, Hq, Hkv, Sq, Sk, D, *qst, *vst, *ost, int(bool(is_causal)),
+                   float(sm_scale), int(num_splits), ws_ptr, ws_bytes, _stream(query))
+        del ws  # stream-ordered reuse, as in _qfused_launch
+    return output
+
+
 # ---- torch.ops.sageattention: the reference's op namespace with its schemas (csrc/pybind_gfx11.cpp:18-47),
 # backed by the functions above (their extra keyword arguments keep their defaults), for callers that use the
 # op namespace directly.  Nothing is registered when the namespace is already taken (for instance by the

@@ -250,6 +250,42 @@ def test_qfused_validation(lib, kw, code, msg):
     assert msg in lib.sage_last_error().decode()
 
 
+def qfused_vrows(lib, **kw):
+    a = dict(q=FAKE, k8=FAKE, v=FAKE, o=FAKE, lse=NULL, ks=FAKE, dtype=0, B=1, Hq=4, Hkv=2, Sq=64, Sk=64, D=128,
+             qsb=4 * 64 * 128, qsh=64 * 128, qsn=128, vsb=2 * 64 * 128, vsh=64 * 128, vsn=128,
+             osb=4 * 64 * 128, osh=64 * 128, osn=128, causal=1, scale=0.125, nsplit=0, ws=NULL, wsb=0, stream=NULL)
+    a.update(kw)
+    return lib.sage_attn_i8_fwd_qfused_vrows(*a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        (dict(dtype=1), _capi.ERR_UNSUPPORTED, "SAGE_DTYPE_F16"),
+        (dict(D=96), _capi.ERR_UNSUPPORTED, "head_dim"),
+        (dict(v=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(v=ODD), _capi.ERR_ALIGNMENT, "q/k/value must be 16-byte aligned"),
+        (dict(vsn=120), _capi.ERR_INVALID_ARG, "V rows must not overlap"),
+        (dict(vsh=-128), _capi.ERR_INVALID_ARG, "value strides"),
+        (dict(vsn=132), _capi.ERR_ALIGNMENT, "value strides must be multiples of 16 bytes"),
+        (dict(vsb=8 * 64 * 128 + 4), _capi.ERR_ALIGNMENT, "value strides"),
+        # per-head V rows addressed with 32-bit offsets: (kv_len + 5 tiles) * row pitch < 4 GiB
+        (dict(Sk=1 << 20, vsn=2048, vsh=2048 * (1 << 20), vsb=2 * 2048 * (1 << 20)), _capi.ERR_UNSUPPORTED,
+         "32-bit"),
+        (dict(qsn=132), _capi.ERR_ALIGNMENT, "16 bytes"),
+        (dict(nsplit=99), _capi.ERR_INVALID_ARG, "num_splits"),
+    ],
+)
+def test_qfused_vrows_validation(lib, kw, code, msg):
+    assert qfused_vrows(lib, **kw) == code
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_qfused_vrows_zero_work_is_ok(lib):
+    assert qfused_vrows(lib, B=0) == _capi.OK
+    assert qfused_vrows(lib, Sq=0) == _capi.OK
+
+
 def test_qfused_zero_work_is_ok(lib):
     assert qfused(lib, Sq=0) == _capi.OK
     assert qfused(lib, B=0, q=NULL) == _capi.OK

@@ -1,0 +1,77 @@
+"""The fused-Q INT8 attention with V read in place (sage_attn_i8_fwd_qfused_vrows, fp16 only) against the V_T
+path it replaces (v_transpose + sage_attn_i8_fwd_qfused, reference core.py:173-179,190-197): the P.V MFMAs see
+the same fp16 V values in the same key order, so output and LSE must match bit for bit -- at the BASELINE fp16
+configs (C2, C4 at full size), ragged and cross lengths, GQA, both layouts, a strided V view, causal and
+non-causal, unsplit and key-split plans.  Every output element starts as NaN (all must be written).  The V_T
+path itself is tied to the oracle by test_gpu_parity / test_gpu_product."""
+import pytest
+import torch
+
+from _helpers import C2, C4, Config, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    C2,
+    C4,
+    Config("ragged1000_d128_causal_hnd", 1, 4, 2, 1000, 128, "fp16", "HND", True, False),
+    Config("ragged300_d64_nhd", 2, 3, 3, 300, 64, "fp16", "NHD", False, False),
+    Config("ragged1000_d64_causal_nhd", 1, 4, 4, 1000, 64, "fp16", "NHD", True, False),
+    Config("cross_q300_kv1000_d128", 1, 4, 4, 1000, 128, "fp16", "HND", False, False, Sq=300),
+    Config("cross_q1000_kv77_d64", 1, 2, 2, 77, 64, "fp16", "NHD", False, False, Sq=1000),
+    Config("gqa_d64_nhd_2304", 1, 20, 5, 2304, 64, "fp16", "NHD", False, False),
+    Config("persistent_causal_d128", 1, 8, 8, 9000, 128, "fp16", "HND", True, False),
+]
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _run(cfg, q, k, v, splits, v_strided=False):
+    from sageattention import ops
+
+    lay = ops.HND if cfg.layout == "HND" else ops.NHD
+    k8, ks = ops.quant_k_int8(k, torch.empty(0, device="cuda", dtype=k.dtype), lay)
+    vt = torch.empty(cfg.B, cfg.Hkv, cfg.D, (cfg.S + 63) // 64 * 64, device="cuda", dtype=torch.float16)
+    ops.v_transpose(v, vt, lay)
+    nan = float("nan")
+    o_ref = torch.full_like(q, nan)
+    lse_ref = torch.full((cfg.B, cfg.Hq, cfg.q_len), nan, device="cuda", dtype=torch.float32)
+    ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o_ref, ks, lay, int(cfg.causal), cfg.D ** -0.5, lse=lse_ref,
+                                      num_splits=splits)
+    if v_strided:
+        # the same V values in a wider buffer: rows 2*D apart (HND) / heads 2*D apart (NHD)
+        wide = torch.zeros(v.shape[:-1] + (2 * cfg.D,), device="cuda", dtype=v.dtype)
+        wide[..., cfg.D // 2: cfg.D // 2 + cfg.D] = v
+        v = wide[..., cfg.D // 2: cfg.D // 2 + cfg.D]
+        assert not v.is_contiguous()
+    o = torch.full_like(q, nan)
+    lse = torch.full((cfg.B, cfg.Hq, cfg.q_len), nan, device="cuda", dtype=torch.float32)
+    ops.qk_int8_sv_f16_attn_qfused_vrows(q, k8, v, o, ks, lay, int(cfg.causal), cfg.D ** -0.5, lse=lse,
+                                         num_splits=splits)
+    torch.cuda.synchronize()
+    return o_ref, lse_ref, o, lse
+
+
+@pytest.mark.parametrize("cfg", CASES, ids=lambda c: c.name)
+@pytest.mark.parametrize("splits", [0, 1, 3])
+def test_vrows_equals_vt_path(cfg, splits):
+    if cfg.S >= 16384 and splits == 3:
+        pytest.skip("causal full-size config: num_splits is ignored (covered by splits 0 and 1)")
+    _say(f"[vrows] {cfg} splits={splits}")
+    q, k, v = (t.cuda() for t in make_inputs(cfg, seed=5))
+    o_ref, lse_ref, o, lse = _run(cfg, q, k, v, splits)
+    assert not bool(torch.isnan(o).any()), f"{int(torch.isnan(o).sum())} output elements unwritten"
+    assert bool(torch.isfinite(lse).all()), "LSE element left unwritten"
+    assert torch.equal(o, o_ref), f"max diff {(o.float() - o_ref.float()).abs().max().item()}"
+    assert torch.equal(lse, lse_ref)
+
+
+@pytest.mark.parametrize("cfg", [CASES[2], CASES[3]], ids=lambda c: c.name)
+def test_vrows_strided_value(cfg):
+    _say(f"[vrows strided V] {cfg}")
+    q, k, v = (t.cuda() for t in make_inputs(cfg, seed=6))
+    o_ref, lse_ref, o, lse = _run(cfg, q, k, v, 0, v_strided=True)
+    assert torch.equal(o, o_ref)
+    assert torch.equal(lse, lse_ref)
