@@ -169,7 +169,7 @@ def cpu_baseline(cfg, budget_s):
         "kind": "port",
         "sample": (f"PyTorch CPU implementation of the quantized path (oracle/torch_cpu.py) on {nh} of {B * Hq} "
                    f"query heads (all {S} rows, {'causal' if causal else 'non-causal'}), median of 3 runs after "
-                   f"1 warm-up: {t_med:.2f} s, scaled x{B * Hq / nh:.0f} to the workload"),
+                   f"1 warm-up: {t_med:.2f} s, scaled x{B * Hq / nh:.3g} to the workload"),
         "threads": torch.get_num_threads(),
         "parallel_info": [ln.strip() for ln in info if ln.strip()][:8],
     }
