@@ -91,6 +91,77 @@ def make_inputs(cfg, device, name=None):
     return q.to(dtype), k.to(dtype), v.to(dtype)
 
 
+class SclkSampler:
+    """Samples the GPU's current shader clock as the driver reports it in sysfs (hwmon freq1_input, else the
+    starred line of pp_dpm_sclk, "S: <MHz>" on MI355X) in a background thread while a timed loop runs; the card
+    is the one whose PCI address is the device's.  Each read queries the SMU (~5 ms), and its value averages
+    over a window that includes the gaps between launches, so it reads lower than the clock inside a kernel
+    (measured with s_memtime / s_memrealtime stamps: ~1.85 GHz under the NS attention kernel).  Reports the
+    median sample in MHz, or None where the files are not readable."""
+
+    def __init__(self, dev):
+        import glob
+        import torch
+
+        self.path, self.kind, self.samples = None, None, []
+        props = torch.cuda.get_device_properties(dev)
+        want = f"{props.pci_domain_id:04x}:{props.pci_bus_id:02x}:{props.pci_device_id:02x}"
+        for card in sorted(glob.glob("/sys/class/drm/card*/device")):
+            try:
+                with open(os.path.join(card, "uevent")) as f:
+                    slot = next((ln.split("=", 1)[1].strip() for ln in f if ln.startswith("PCI_SLOT_NAME=")), "")
+            except OSError:
+                continue
+            if not slot.lower().startswith(want):
+                continue
+            hw = sorted(glob.glob(os.path.join(card, "hwmon", "hwmon*", "freq1_input")))
+            if hw:
+                self.path, self.kind = hw[0], "hwmon"
+            elif os.path.exists(os.path.join(card, "pp_dpm_sclk")):
+                self.path, self.kind = os.path.join(card, "pp_dpm_sclk"), "dpm"
+            break
+
+    def _read(self):
+        try:
+            with open(self.path) as f:
+                text = f.read()
+        except OSError:
+            return None
+        if self.kind == "hwmon":
+            return int(text.strip()) / 1e6
+        for ln in text.splitlines():
+            if ln.strip().endswith("*"):
+                return float(ln.split(":")[1].strip().rstrip("*").strip().lower().rstrip("mhz"))
+        return None
+
+    def __enter__(self):
+        import threading
+
+        self._stop = threading.Event()
+
+        def run():
+            while not self._stop.wait(0.005):
+                v = self._read()
+                if v is not None:
+                    self.samples.append(v)
+
+        if self.path:
+            self._t = threading.Thread(target=run, daemon=True)
+            self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self.path:
+            self._t.join()
+
+    def mhz(self):
+        if not self.samples:
+            return None
+        v = sorted(self.samples)
+        return round(v[len(v) // 2], 1)
+
+
 def queue_ahead(dev):
     """Occupy the GPU for about 2 ms (a fill of 12 GiB, HBM-bound, not MFMA: a matmul here lowers the clock
     for the next ~20 ms of MFMA work) so that the host can enqueue a whole timed loop while it runs: the
@@ -542,15 +613,18 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done")
 
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
+    sampler = SclkSampler(dev)
+    with sampler:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
     ops_step = attn_ops(B, Hq, S, S, D, causal)
     value = ops_step / (ms_step * 1e-3) / 1e12
-    log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS")
+    log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS; shader clock during the "
+        f"steps (sysfs) {sampler.mhz()} MHz ({sampler.kind or 'not readable'}, {len(sampler.samples)} samples)")
 
     # ---- per-kernel timing with HIP events on the launch stream
     lay = ops.HND if layout == "HND" else ops.NHD
@@ -681,7 +755,9 @@ def main():
         "direct": direct,
         "configs": configs,
         "reference_shapes": ref_shapes,
-        "device": {"name": props.name, "cus": props.multi_processor_count},
+        "device": {"name": props.name, "cus": props.multi_processor_count,
+                   "sclk_mhz_sysfs_during_steps": sampler.mhz(), "sclk_source": sampler.kind,
+                   "peak_clock_assumed_mhz": 2400},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
