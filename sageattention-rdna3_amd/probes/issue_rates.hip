@@ -21,6 +21,7 @@
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -35,12 +36,26 @@ enum Kind {
   kMixLds,       // kMix with each MFMA's A operand read from LDS two MFMAs ahead, as the key loop reads K and V
   kRoles,        // the same work as kMix split by role: waves 0-3 of the block issue only the MFMAs (8 per
                  // iteration), waves 4+ (sharing the SIMDs) only the VALU part (44 fma + 12 exp per iteration)
+  kMfmaF16Acc,   // kMfmaF16 with the accumulators in AGPRs
+  kMixAcc,       // kMix with the MFMA accumulators in AGPRs
+  kMixHalf,      // 4 MFMA f16 + 11 fma + 3 exp: half the VALU of kMix
+  kMixFma,       // 4 MFMA f16 + 22 fma: kMix without its exponentials
+  kMfma16,       // 4 x v_mfma_f32_16x16x32_f16 (half the work of the 32x32x16 MFMA each)
+  kMix16,        // 8 x v_mfma_f32_16x16x32_f16 + 22 fma + 6 exp: kMix's work with the 16x16 MFMA shape
+  kExpF16,       // 24 x v_exp_f16
+  kMix2,         // 2 MFMA f16 + 22 fma + 6 exp: the D = 64 key loop's ratio (12 MFMA : 135 VALU : 33 exp)
+  kMfmaDep,      // 4 x v_mfma_f32_32x32x16_f16 on one accumulator (each reads the previous result)
+  kMixSalu,      // kMix + 12 s_add_u32 (the key loop issues ~11 SALU per 4 MFMAs)
   kKinds
 };
-constexpr int kUnitOps[kKinds] = {4, 4, 24, 24, 4, 4, 4, 4};
+constexpr int kUnitOps[kKinds] = {4, 4, 24, 24, 4, 4, 4, 4, 4, 4, 4, 4, 4, 8, 24, 2, 4, 4};
 const char* kNames[kKinds] = {"v_mfma_f32_32x32x16_f16", "v_mfma_i32_32x32x32_i8", "v_fma_f32", "v_exp_f32",
                               "mix: 4 MFMA f16 + 22 fma + 6 exp", "ds_read_b128", "mix + 4 ds_read_b128 operands",
-                              "mix work split: MFMA waves + VALU waves"};
+                              "mix work split: MFMA waves + VALU waves",
+                              "v_mfma_f32_32x32x16_f16, AGPR acc", "mix, MFMA accumulators in AGPRs",
+                              "4 MFMA f16 + 11 fma + 3 exp", "4 MFMA f16 + 22 fma", "v_mfma_f32_16x16x32_f16",
+                              "8 MFMA 16x16x32 + 22 fma + 6 exp", "v_exp_f16",
+                              "2 MFMA f16 + 22 fma + 6 exp", "v_mfma_f32_32x32x16_f16, one chain", "mix + 12 SALU"};
 
 #define FMA4 "v_fma_f32 %4, %4, %12, %13\n v_fma_f32 %5, %5, %12, %13\n v_fma_f32 %6, %6, %12, %13\n v_fma_f32 %7, %7, %12, %13\n"
 #define FMA2 "v_fma_f32 %8, %8, %12, %13\n v_fma_f32 %9, %9, %12, %13\n"
@@ -66,6 +81,9 @@ __global__ __launch_bounds__(1024) void unit_loop(int iters, unsigned long long*
   }
   f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
   i32x16 d0 = {}, d1 = {}, d2 = {}, d3 = {};
+  f32x4 e0 = {}, e1 = {}, e2 = {}, e3 = {};
+  _Float16 h0 = static_cast<_Float16>(threadIdx.x & 7), h1 = h0 + static_cast<_Float16>(1), h2 = -h0, h3 = -h1,
+           h4 = h0 * static_cast<_Float16>(0.5f), h5 = h1 * static_cast<_Float16>(0.25f);
   const i32x4 ia = {static_cast<int>(threadIdx.x), 1, 2, 3}, ib = {5, 6, 7, 8};
   float x0 = threadIdx.x, x1 = x0 + 1, x2 = x0 + 2, x3 = x0 + 3, x4 = x0 + 4, x5 = x0 + 5, x6 = -1.0f, x7 = -2.0f;
   const float m = 0.999f, k = 0.001f;
@@ -80,6 +98,87 @@ __global__ __launch_bounds__(1024) void unit_loop(int iters, unsigned long long*
           "v_mfma_f32_32x32x16_f16 %2, %4, %5, %2\n v_mfma_f32_32x32x16_f16 %3, %4, %5, %3\n"
           : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3)
           : "v"(a), "v"(b));
+    } else if constexpr (KIND == kMfmaF16Acc) {
+      asm volatile(
+          "v_mfma_f32_32x32x16_f16 %0, %4, %5, %0\n v_mfma_f32_32x32x16_f16 %1, %4, %5, %1\n"
+          "v_mfma_f32_32x32x16_f16 %2, %4, %5, %2\n v_mfma_f32_32x32x16_f16 %3, %4, %5, %3\n"
+          : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3)
+          : "v"(a), "v"(b));
+    } else if constexpr (KIND == kMixAcc) {
+      asm volatile(
+          "v_mfma_f32_32x32x16_f16 %0, %14, %15, %0\n" FMA4 "v_fma_f32 %8, %8, %12, %13\n" EXP2
+          "v_mfma_f32_32x32x16_f16 %1, %14, %15, %1\n" FMA4 FMA2 "v_exp_f32 %10, %10\n"
+          "v_mfma_f32_32x32x16_f16 %2, %14, %15, %2\n" FMA4 "v_fma_f32 %9, %9, %12, %13\n" EXP2
+          "v_mfma_f32_32x32x16_f16 %3, %14, %15, %3\n" FMA4 FMA2 "v_exp_f32 %11, %11\n"
+          : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3), "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3), "+v"(x4), "+v"(x5),
+            "+v"(x6), "+v"(x7)
+          : "v"(m), "v"(k), "v"(a), "v"(b));
+    } else if constexpr (KIND == kMixHalf) {
+      asm volatile(
+          "v_mfma_f32_32x32x16_f16 %0, %14, %15, %0\n" FMA2 "v_exp_f32 %10, %10\n"
+          "v_mfma_f32_32x32x16_f16 %1, %14, %15, %1\n" FMA4 "v_fma_f32 %8, %8, %12, %13\n"
+          "v_mfma_f32_32x32x16_f16 %2, %14, %15, %2\n" FMA2 "v_exp_f32 %11, %11\n"
+          "v_mfma_f32_32x32x16_f16 %3, %14, %15, %3\n" "v_fma_f32 %9, %9, %12, %13\n v_fma_f32 %4, %4, %12, %13\n"
+          "v_exp_f32 %10, %10\n" OPERANDS);
+    } else if constexpr (KIND == kMixFma) {
+      asm volatile(
+          "v_mfma_f32_32x32x16_f16 %0, %14, %15, %0\n" FMA4 "v_fma_f32 %8, %8, %12, %13\n"
+          "v_mfma_f32_32x32x16_f16 %1, %14, %15, %1\n" FMA4 FMA2
+          "v_mfma_f32_32x32x16_f16 %2, %14, %15, %2\n" FMA4 "v_fma_f32 %9, %9, %12, %13\n"
+          "v_mfma_f32_32x32x16_f16 %3, %14, %15, %3\n" FMA4 FMA2 OPERANDS);
+    } else if constexpr (KIND == kMfma16) {
+      asm volatile(
+          "v_mfma_f32_16x16x32_f16 %0, %4, %5, %0\n v_mfma_f32_16x16x32_f16 %1, %4, %5, %1\n"
+          "v_mfma_f32_16x16x32_f16 %2, %4, %5, %2\n v_mfma_f32_16x16x32_f16 %3, %4, %5, %3\n"
+          : "+v"(e0), "+v"(e1), "+v"(e2), "+v"(e3)
+          : "v"(a), "v"(b));
+    } else if constexpr (KIND == kMix16) {
+      asm volatile(
+          "v_mfma_f32_16x16x32_f16 %0, %14, %15, %0\n" FMA4 "v_mfma_f32_16x16x32_f16 %1, %14, %15, %1\n"
+          "v_fma_f32 %8, %8, %12, %13\n" EXP2
+          "v_mfma_f32_16x16x32_f16 %2, %14, %15, %2\n" FMA4 "v_mfma_f32_16x16x32_f16 %3, %14, %15, %3\n"
+          FMA2 "v_exp_f32 %10, %10\n"
+          "v_mfma_f32_16x16x32_f16 %0, %14, %15, %0\n" FMA4 "v_mfma_f32_16x16x32_f16 %1, %14, %15, %1\n"
+          "v_fma_f32 %9, %9, %12, %13\n" EXP2
+          "v_mfma_f32_16x16x32_f16 %2, %14, %15, %2\n" FMA4 "v_mfma_f32_16x16x32_f16 %3, %14, %15, %3\n"
+          FMA2 "v_exp_f32 %11, %11\n"
+          : "+v"(e0), "+v"(e1), "+v"(e2), "+v"(e3), "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3), "+v"(x4), "+v"(x5),
+            "+v"(x6), "+v"(x7)
+          : "v"(m), "v"(k), "v"(a), "v"(b));
+    } else if constexpr (KIND == kExpF16) {
+      asm volatile(
+          "v_exp_f16 %0, %0\n v_exp_f16 %1, %1\n v_exp_f16 %2, %2\n v_exp_f16 %3, %3\n v_exp_f16 %4, %4\n"
+          "v_exp_f16 %5, %5\n v_exp_f16 %0, %0\n v_exp_f16 %1, %1\n v_exp_f16 %2, %2\n v_exp_f16 %3, %3\n"
+          "v_exp_f16 %4, %4\n v_exp_f16 %5, %5\n v_exp_f16 %0, %0\n v_exp_f16 %1, %1\n v_exp_f16 %2, %2\n"
+          "v_exp_f16 %3, %3\n v_exp_f16 %4, %4\n v_exp_f16 %5, %5\n v_exp_f16 %0, %0\n v_exp_f16 %1, %1\n"
+          "v_exp_f16 %2, %2\n v_exp_f16 %3, %3\n v_exp_f16 %4, %4\n v_exp_f16 %5, %5\n"
+          : "+v"(h0), "+v"(h1), "+v"(h2), "+v"(h3), "+v"(h4), "+v"(h5));
+    } else if constexpr (KIND == kMix2) {
+      asm volatile(
+          "v_mfma_f32_32x32x16_f16 %0, %14, %15, %0\n" FMA4 "v_fma_f32 %8, %8, %12, %13\n" EXP2
+          FMA4 FMA2 "v_exp_f32 %10, %10\n"
+          "v_mfma_f32_32x32x16_f16 %1, %14, %15, %1\n" FMA4 "v_fma_f32 %9, %9, %12, %13\n" EXP2
+          FMA4 FMA2 "v_exp_f32 %11, %11\n" OPERANDS);
+    } else if constexpr (KIND == kMfmaDep) {
+      asm volatile(
+          "v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n"
+          "v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n"
+          : "+v"(c0)
+          : "v"(a), "v"(b));
+    } else if constexpr (KIND == kMixSalu) {
+      asm volatile(
+          "v_mfma_f32_32x32x16_f16 %0, %14, %15, %0\n" FMA4 "s_add_u32 s90, s90, 1\n s_add_u32 s91, s91, 3\n"
+          "v_fma_f32 %8, %8, %12, %13\n s_add_u32 s90, s90, 5\n" EXP2
+          "v_mfma_f32_32x32x16_f16 %1, %14, %15, %1\n" FMA4 "s_add_u32 s91, s91, 1\n s_add_u32 s90, s90, 3\n"
+          FMA2 "s_add_u32 s91, s91, 5\n v_exp_f32 %10, %10\n"
+          "v_mfma_f32_32x32x16_f16 %2, %14, %15, %2\n" FMA4 "s_add_u32 s90, s90, 1\n s_add_u32 s91, s91, 3\n"
+          "v_fma_f32 %9, %9, %12, %13\n s_add_u32 s90, s90, 5\n" EXP2
+          "v_mfma_f32_32x32x16_f16 %3, %14, %15, %3\n" FMA4 "s_add_u32 s91, s91, 1\n s_add_u32 s90, s90, 3\n"
+          FMA2 "s_add_u32 s91, s91, 5\n v_exp_f32 %11, %11\n"
+          : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3), "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3), "+v"(x4), "+v"(x5),
+            "+v"(x6), "+v"(x7)
+          : "v"(m), "v"(k), "v"(a), "v"(b)
+          : "s90", "s91", "scc");
     } else if constexpr (KIND == kMfmaI8) {
       asm volatile(
           "v_mfma_i32_32x32x32_i8 %0, %4, %5, %0\n v_mfma_i32_32x32x32_i8 %1, %4, %5, %1\n"
@@ -145,6 +244,8 @@ __global__ __launch_bounds__(1024) void unit_loop(int iters, unsigned long long*
   const unsigned long long t1 = __builtin_amdgcn_s_memtime();
   float s = x0 + x1 + x2 + x3 + x4 + x5 + x6 + x7 + static_cast<float>(a[0] + a1[1] + a2[2]);
   for (int i = 0; i < 16; ++i) s += c0[i] + c1[i] + c2[i] + c3[i] + static_cast<float>(d0[i] + d1[i] + d2[i] + d3[i]);
+  for (int i = 0; i < 4; ++i) s += e0[i] + e1[i] + e2[i] + e3[i];
+  s += static_cast<float>(h0 + h1 + h2 + h3 + h4 + h5);
   sink[blockIdx.x * blockDim.x + threadIdx.x] = s;
   if ((threadIdx.x & 63) == 0) {
     const int w = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
@@ -178,6 +279,11 @@ __global__ __launch_bounds__(256) void clock_pair(int iters, unsigned long long*
     out[2 * blockIdx.x] = m1 - m0;
     out[2 * blockIdx.x + 1] = r1 - r0;
   }
+}
+
+static bool per_unit_kind(int kind) {
+  return kind == kMix || kind == kMixLds || kind == kMixAcc || kind == kMixHalf || kind == kMixFma || kind == kMix16 ||
+         kind == kMix2 || kind == kMixSalu;
 }
 
 #define CHECK(x)                                                      \
@@ -229,6 +335,16 @@ int main() {
           case kLds: unit_loop<kLds><<<cus, 256 * W>>>(iters, t, sink); break;
           case kMixLds: unit_loop<kMixLds><<<cus, 256 * W>>>(iters, t, sink); break;
           case kRoles: unit_loop<kRoles><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMfmaF16Acc: unit_loop<kMfmaF16Acc><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMixAcc: unit_loop<kMixAcc><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMixHalf: unit_loop<kMixHalf><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMixFma: unit_loop<kMixFma><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMfma16: unit_loop<kMfma16><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMix16: unit_loop<kMix16><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kExpF16: unit_loop<kExpF16><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMix2: unit_loop<kMix2><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMfmaDep: unit_loop<kMfmaDep><<<cus, 256 * W>>>(iters, t, sink); break;
+          case kMixSalu: unit_loop<kMixSalu><<<cus, 256 * W>>>(iters, t, sink); break;
           default: unit_loop<kMix><<<cus, 256 * W>>>(iters, t, sink); break;
         }
       };
@@ -253,11 +369,11 @@ int main() {
       const double per_unit = kind == kRoles ? span / (static_cast<double>(iters) * 2)
                                              : span / (static_cast<double>(iters) * W);
       unit[kind][W] = per_unit;
-      const bool per_u = kind == kMix || kind == kMixLds || kind == kRoles;
+      const bool per_u = kind == kRoles || per_unit_kind(kind);
       printf(" %7.2f", per_u ? per_unit : per_unit / kUnitOps[kind]);
     }
     printf("   %s\n", kind == kRoles ? "(per unit of MFMA work; W=2 is the balanced 1:1 split)"
-                     : (kind == kMix || kind == kMixLds) ? "(per unit)" : "(per instruction)");
+                     : per_unit_kind(kind) ? "(per unit)" : "(per instruction)");
     if (kind == kLds) {
       // per SIMD, one wave's unit (4 KB) per per_unit cycles; 4 SIMDs per CU
       printf("%-36s", "  = LDS bytes read per clock per CU");
