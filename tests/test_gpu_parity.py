@@ -152,6 +152,40 @@ def test_large_scales_take_the_exact_softmax(causal):
     _say(f"  worst |gpu-oracle| = {worst:.3g}")
 
 
+GROWING = [
+    Config("grow_d128_causal", 1, 4, 2, 1000, 128, "bf16", "HND", True, False),
+    Config("grow_d128_nhd", 1, 4, 4, 777, 128, "fp16", "NHD", False, False),
+    Config("grow_d64", 1, 4, 4, 1100, 64, "fp16", "HND", False, False),
+]
+
+
+@pytest.mark.parametrize("cfg", GROWING, ids=lambda c: c.name)
+def test_growing_scores_move_the_reference_max(cfg):
+    """Keys whose magnitude grows 4x per 64-key tile over the first six tiles make every row's max
+    jump by far more than 2^8 (in p) from one tile to the next, and then keys of one tile repeat
+    four rows, so that many p of a tile are equal.  The INT8 key loop tests the lazy max on each
+    lane's tile sum after the exponentials and redoes a tile whose sum passes 2^8 with the
+    reference max moved; every row is held to the oracle bar, and the fused-Q kernel to the
+    two-kernel path bit for bit."""
+    _say(f"[growing] {cfg}")
+    q, k, v = (t.float() for t in make_inputs(cfg, seed=11))
+    kh = orc.to_hnd(k.numpy(), cfg.layout).copy()
+    n = np.arange(cfg.S)
+    kh *= (4.0 ** np.minimum(n // 64, 5))[None, None, :, None]
+    # keys 384.. of each tile: rows 4r..4r+3 equal (many equal p per lane)
+    rep = (n >= 384) & (n % 4 != 0)
+    kh[:, :, rep] = kh[:, :, n[rep] // 4 * 4]
+    k = torch.from_numpy(kh if cfg.layout == "HND" else kh.transpose(0, 2, 1, 3).copy())
+    q, k, v = (t.to(torch.bfloat16 if cfg.dtype == "bf16" else torch.float16) for t in (q, k, v))
+    pro = gpu_prologue(cfg, q, k, v)
+    assert float(pro["q_scale"].max()) * float(pro["k_scale"].max()) < 0.49  # the conversion-free loop
+    o = gpu_attn(cfg, pro, q.dtype)
+    worst = check_rows_vs_oracle(cfg, pro, o, range(cfg.Hq), np.arange(cfg.q_len), cfg.dtype)
+    o_f, _, _, _ = gpu_fused(cfg, q, k, v)
+    assert torch.equal(o_f, o)
+    _say(f"  worst |gpu-oracle| = {worst:.3g}")
+
+
 # ------------------------------------------------------------------ Q quantisation fused into the attention kernel
 def gpu_fused(cfg: Config, q, k, v, with_lse=False):
     """K quant + V layout + attention with Q quantised inside the kernel (the ``sageattn`` INT8 path),
