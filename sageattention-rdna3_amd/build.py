@@ -1,10 +1,12 @@
 """Build the gfx950 C-ABI library ``sageattention/libsage_mi355x.so`` and the compiled host layer of
 ``sageattn`` (``sageattention/_sage_host.so``, linked against it) in-tree.
 
-Usage: ``python sageattention-rdna3_amd/build.py [-v] [--asan]``.  Cross-compiles
-for gfx950 with hipcc; no GPU is needed.  Every call recompiles.  ``--asan``
-builds the host-AddressSanitizer variant of the library instead
-(``_build_asan/``, for the C-ABI tests on the CPU).
+Usage: ``python sageattention-rdna3_amd/build.py [-v] [--asan | --stamps]``.
+Cross-compiles for gfx950 with hipcc; no GPU is needed.  Every call recompiles.
+``--asan`` builds the host-AddressSanitizer variant of the library instead
+(``_build_asan/``, for the C-ABI tests on the CPU); ``--stamps`` the variant
+whose attention kernels record per-wave cycle stamps (``_build_stamps/``, read
+by ``stamps.py``).
 
 Flags:
   * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` on every device
@@ -161,8 +163,36 @@ def build_asan(verbose: bool = False) -> str:
     return ASAN_LIB
 
 
+# Cycle-stamps build of the library: the attention kernels compiled with SAGE_STAMPS=1 (per-wave s_memtime
+# counts of item phases and key-loop steps, csrc/attn_body.inc) plus sage_stamps_read / sage_stamps_clear.
+# Loaded through SAGEATTN_MI355X_LIB by stamps.py; never the product library.
+STAMPS_DIR = os.path.join(HERE, "_build_stamps")
+STAMPS_LIB = os.path.join(STAMPS_DIR, "libsage_mi355x_stamps.so")
+
+
+def build_stamps(verbose: bool = False) -> str:
+    """Build STAMPS_LIB; returns its path."""
+    os.makedirs(STAMPS_DIR, exist_ok=True)
+    jobs, objs = [], []
+    for src, extra in SOURCES:
+        obj = os.path.join(STAMPS_DIR, os.path.splitext(src)[0] + ".o")
+        cmd = [HIPCC, *COMMON, *extra, "-DSAGE_STAMPS=1", "-c", os.path.join(CSRC, src), "-o", obj]
+        if src.endswith(".cpp"):
+            cmd[1:1] = ["-x", "hip"]
+        jobs.append((cmd, _start(cmd, verbose)))
+        objs.append(obj)
+    for cmd, proc in jobs:
+        _finish(cmd, proc, verbose)
+    tmp = STAMPS_LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    os.replace(tmp, STAMPS_LIB)
+    return STAMPS_LIB
+
+
 if __name__ == "__main__":
     if "--asan" in sys.argv:
         print(build_asan(verbose="-v" in sys.argv))
+    elif "--stamps" in sys.argv:
+        print(build_stamps(verbose="-v" in sys.argv))
     else:
         print(build(verbose="-v" in sys.argv))

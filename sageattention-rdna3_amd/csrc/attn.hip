@@ -98,6 +98,18 @@ int device_cus() {
 // S4096: 65.9 -> 56.2 us); causal launches +3% to +6% and D = 128 non-causal
 // launches with key splits +3% to +4% (the doubled tile traffic), so those
 // stay on w8.  The D = 128 direct kernel's 98 KB of LDS would not fit twice.
+// The stamps build (build.py --stamps, SAGE_STAMPS=1) adds per-wave cycle
+// stamps to the attention kernels (attn_body.inc, StampField) and the two
+// functions below that read them; the default build has neither.
+#ifndef SAGE_STAMPS
+#define SAGE_STAMPS 0
+#endif
+#if SAGE_STAMPS
+constexpr int kStampBlocks = 2048;  // blocks whose waves record (8 waves each at most)
+constexpr int kStampStride = 32;    // uint64 fields per wave record
+__device__ uint64_t g_stamps[kStampBlocks * 8 * kStampStride];
+#endif
+
 namespace w8 {
 constexpr int kBM = 256;
 constexpr int kWaves = 8;
@@ -303,3 +315,19 @@ extern "C" int sage_attn_split_plan(int quantized, int64_t batch, int64_t q_head
       split_plan(quantized != 0, batch, q_heads, q_len, kv_len, head_dim, is_causal, num_splits, whole_qblocks, splits);
   return r < 0 ? static_cast<int>(r) : SAGE_OK;
 }
+
+#if SAGE_STAMPS
+// Stamps build only: copy `bytes` of the wave records (kStampStride uint64
+// fields per wave, block-major) to host memory / clear them.
+extern "C" int sage_stamps_read(void* host, size_t bytes) {
+  if (bytes > sizeof(sage::g_stamps)) return SAGE_ERR_INVALID_ARG;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(sage::g_stamps), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess
+             ? SAGE_OK
+             : SAGE_ERR_HIP;
+}
+extern "C" int sage_stamps_clear(void) {
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(sage::g_stamps)) != hipSuccess) return SAGE_ERR_HIP;
+  return hipMemset(ptr, 0, sizeof(sage::g_stamps)) == hipSuccess ? SAGE_OK : SAGE_ERR_HIP;
+}
+#endif
