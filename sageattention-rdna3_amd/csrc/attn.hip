@@ -36,7 +36,10 @@
 //     rewritten in place: the chunk order reads each before overwriting it;
 //   * online softmax with a lazy reference max: the max moves only when a row
 //     max grows by more than 2^8; O is then rescaled at the top of the next
-//     step, after the P.V MFMAs that still used the old max;
+//     step, after the P.V MFMAs that still used the old max.  The unmasked
+//     INT8 loop tests each lane's tile sum of p against 2^8 after the
+//     exponentials instead of taking the max first, and redoes the rare tile
+//     that fails with the max moved (TileSoftmaxSum);
 //   * K/V tiles stream into a 3-stage LDS ring with buffer_load ... lds
 //     (no staging registers), issued two steps ahead; loads past the block's
 //     last key read as zero through the descriptor's record count.  The
