@@ -172,6 +172,33 @@ def test_direct_lse_vs_oracle(cfg):
             assert np.all(err <= 2e-4 + 2e-6 * np.abs(ref)), f"b={b} h={h} worst {err.max():.3g}"
 
 
+DIRECT_GROWING = [
+    Config("dgrow_d128_causal", 1, 4, 2, 1000, 128, "bf16", "HND", True, False),
+    Config("dgrow_d128_nhd", 1, 4, 4, 777, 128, "fp16", "NHD", False, False),
+    Config("dgrow_d64", 1, 4, 4, 1100, 64, "fp16", "HND", False, False),
+]
+
+
+@pytest.mark.parametrize("cfg", DIRECT_GROWING, ids=lambda c: c.name)
+def test_direct_growing_scores_move_the_reference_max(cfg):
+    """Keys whose magnitude grows 4x per 64-key tile over the first six tiles (then keys of one tile
+    repeat four rows): every row's max jumps by far more than 2^8 (in p) from tile to tile, so the
+    unmasked loop's tile-sum test fails and the tile is redone with the reference max moved (S from
+    global K).  Every row against the oracle's direct attention."""
+    _say(f"[direct growing] {cfg}")
+    q, k, v = (t.float() for t in make_inputs(cfg, seed=11))
+    kh = orc.to_hnd(k.numpy(), cfg.layout).copy()
+    n = np.arange(cfg.S)
+    kh *= (4.0 ** np.minimum(n // 64, 5))[None, None, :, None]
+    rep = (n >= 384) & (n % 4 != 0)
+    kh[:, :, rep] = kh[:, :, n[rep] // 4 * 4]
+    k = torch.from_numpy(kh if cfg.layout == "HND" else kh.transpose(0, 2, 1, 3).copy())
+    q, k, v = (t.to(torch.bfloat16 if cfg.dtype == "bf16" else torch.float16) for t in (q, k, v))
+    o, _, vt = gpu_direct(cfg, q, k, v)
+    worst = check_direct_rows(cfg, q, k, vt, o, range(cfg.Hq), np.arange(cfg.q_len), cfg.D ** -0.5)
+    _say(f"  worst |gpu-oracle| = {worst:.3g}")
+
+
 def test_direct_empty_kv_and_zero_rows():
     """kv_len = 0: zero output and -inf LSE (no key); q_len = 0 is a no-op."""
     from sageattention import ops
