@@ -282,6 +282,28 @@ int sage_attn_direct_fwd(const void* query, const void* key, const void* value_t
                          int is_causal, double sm_scale, int num_splits, void* workspace,
                          int64_t workspace_bytes, void* stream);
 
+/*
+ * sage_attn_direct_fwd for fp16 inputs with V read in place: `value` is the
+ * caller's fp16 V [B,Hkv,Sk,D] through its strides (HND or NHD; 16-byte
+ * aligned base, strides multiples of 8 elements, rows not overlapping) instead
+ * of a V_T from sage_v_layout, so the short-sequence branch is one launch
+ * (the kernel transposes V tiles in LDS with ds_read_b64_tr_b16).  dtype must
+ * be SAGE_DTYPE_F16 (Q, K, V and out).  The MFMAs see the same V values in the
+ * same order, so results equal sage_v_layout + sage_attn_direct_fwd bit for
+ * bit.  No single reference counterpart: it replaces v_transpose
+ * (csrc/attn_gfx11.cu:1889-1935, kernel :323-407; sageattention/core.py:153-164)
+ * followed by fp16_attn_t (csrc/pybind_gfx11.cpp:24-31, csrc/attn_gfx11.cu:2275-2472).
+ */
+int sage_attn_direct_fwd_vrows(const void* query, const void* key, const void* value, void* out, float* lse,
+                               int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                               int64_t q_len, int64_t kv_len, int64_t head_dim,
+                               int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                               int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                               int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n,
+                               int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                               int is_causal, double sm_scale, int num_splits, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,9 +37,9 @@
 //   * online softmax with a lazy reference max: the max moves only when a row
 //     max grows by more than 2^8; O is then rescaled at the top of the next
 //     step, after the P.V MFMAs that still used the old max.  The unmasked
-//     INT8 loop tests each lane's tile sum of p against 2^8 after the
-//     exponentials instead of taking the max first, and redoes the rare tile
-//     that fails with the max moved (TileSoftmaxSum);
+//     loop tests each lane's tile sum of p against 2^8 after the exponentials
+//     instead of taking the max first, and redoes the rare tile that fails
+//     with the max moved (TileSoftmaxSum);
 //   * K/V tiles stream into a 3-stage LDS ring with buffer_load ... lds
 //     (no staging registers), issued two steps ahead; loads past the block's
 //     last key read as zero through the descriptor's record count.  The
@@ -234,6 +234,22 @@ extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const vo
                   out, lse, nullptr, nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b,
                   q_stride_h, q_stride_n, k_stride_b, k_stride_h, k_stride_n, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
                   is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_direct_fwd");
+}
+
+extern "C" int sage_attn_direct_fwd_vrows(const void* query, const void* key, const void* value, void* out,
+                                          float* lse, int dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                          int64_t q_len, int64_t kv_len, int64_t head_dim,
+                                          int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_n,
+                                          int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                                          int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n,
+                                          int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
+                                          int is_causal, double sm_scale, int num_splits, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return run_attn(head_dim, is_causal, w8::kQkF16V, query, key, value, out, lse, nullptr, nullptr, dtype, batch,
+                  q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b,
+                  k_stride_h, k_stride_n, v_stride_b, v_stride_h, v_stride_n, o_stride_b, o_stride_h, o_stride_n,
+                  is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_direct_fwd_vrows");
 }
 
 extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* value_t, void* out,

@@ -74,6 +74,10 @@ SIGNATURES = {
                                   _I64, _I64, _I64, _I64, _I64, _I64,
                                   _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                   _I, ctypes.c_double, _I, _P, _I64, _P]),
+    "sage_attn_direct_fwd_vrows": (_I, [_P, _P, _P, _P, _P, _I,
+                                        _I64, _I64, _I64, _I64, _I64, _I64,
+                                        _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                        _I, ctypes.c_double, _I, _P, _I64, _P]),
     "sage_attn_workspace_bytes": (_I64, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I]),
     "sage_attn_split_plan": (_I, [_I, _I64, _I64, _I64, _I64, _I64, _I, _I, _P, _P]),
 }

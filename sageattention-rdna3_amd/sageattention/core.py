@@ -132,7 +132,8 @@ def sageattn(
 
     # the rest of the call (shapes, allocations, the launches of the direct or the INT8 path) in one
     # compiled call over the C ABI (csrc/host_ops.cpp): direct = V transform + fp16_attn_t /
-    # bf16_attn_t (core.py:141-164); INT8 = [K mean] + K quantisation and V transform in one launch +
+    # bf16_attn_t (core.py:141-164), or for fp16 inputs up to a measured key length one launch that reads V
+    # in place (the same output bit for bit); INT8 = [K mean] + K quantisation and V transform in one launch +
     # the attention kernel that quantises Q itself (the q_int8 and q_scale of quant_qk_int8, so the same
     # output).  return_lse: the reference returns a zero placeholder (core.py:203-211); both kernels
     # write the real log-sum-exp of each row (natural log of the scaled scores; -inf without keys).

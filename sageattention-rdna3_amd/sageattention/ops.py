@@ -307,6 +307,43 @@ def bf16_attn_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, out
                           sm_scale, lse, num_splits)
 
 
+def fp16_attn_vrows(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, output: torch.Tensor,
+                    tensor_layout: int, is_causal: int, sm_scale: float,
+                    lse: Optional[torch.Tensor] = None, num_splits: int = 0) -> torch.Tensor:
+    """:func:`fp16_attn_t` with ``value`` the caller's fp16 V itself (``[B, Hkv, Sk, D]`` in
+    ``tensor_layout``, read through its strides) instead of a V_T from :func:`v_transpose`: the kernel
+    transposes V tiles in LDS, so the short-sequence branch is one launch.  Same result bit for bit as
+    ``v_transpose`` followed by :func:`fp16_attn_t`.  This build's fusion; it replaces the reference's
+    v_transpose + fp16_attn_t pair (core.py:141-164) for fp16 inputs."""
+    op = "fp16_attn_vrows"
+    for name, t in (("query", query), ("key", key), ("value", value), ("output", output)):
+        if t.dtype != torch.float16:
+            raise ValueError(f"{op}: {name} must be torch.float16, got {t.dtype}")
+        if t.dim() != 4 or t.stride(-1) != 1:
+            raise ValueError(f"{op}: {name} must be 4-D with a contiguous head_dim axis")
+    (B, Hq, Sq, D), qst = _bhnd(query, tensor_layout)
+    (Bk, Hkv, Sk, Dk), kst = _bhnd(key, tensor_layout)
+    if Bk != B or Dk != D:
+        raise ValueError(f"{op}: query {tuple(query.shape)} and key {tuple(key.shape)} disagree")
+    (Bv, Hv, Sv, Dv), vst = _bhnd(value, tensor_layout)
+    if (Bv, Hv, Sv, Dv) != (B, Hkv, Sk, D):
+        raise ValueError(f"{op}: value must be [{B},{Hkv},{Sk},{D}] in the tensor layout")
+    (Bo, Ho, So, Do), ost = _bhnd(output, tensor_layout)
+    if (Bo, Ho, So, Do) != (B, Hq, Sq, D):
+        raise ValueError(f"{op}: output shape does not match the query")
+    if lse is not None:
+        if tuple(lse.shape) != (B, Hq, Sq) or lse.dtype != torch.float32 or not lse.is_contiguous():
+            raise ValueError(f"{op}: lse must be contiguous fp32 [{B},{Hq},{Sq}]")
+    with _on_device(query.device):
+        ws, ws_ptr, ws_bytes = _split_workspace(False, B, Hq, Sq, Sk, D, is_causal, num_splits, query.device)
+        _capi.call("sage_attn_direct_fwd_vrows", query.data_ptr(), key.data_ptr(), value.data_ptr(),
+                   output.data_ptr(), lse.data_ptr() if lse is not None else _NULL, _dtype_code(query), B, Hq, Hkv,
+                   Sq, Sk, D, *qst, *kst, *vst, *ost, int(bool(is_causal)), float(sm_scale), int(num_splits),
+                   ws_ptr, ws_bytes, _stream(query))
+        del ws  # stream-ordered reuse, as in _direct_launch
+    return output
+
+
 def qk_int8_sv_bf16_attn_qfused_t(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                                   output: torch.Tensor, k_scale: torch.Tensor, tensor_layout: int,
                                   is_causal: int, sm_scale: float,

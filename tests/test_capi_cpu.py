@@ -286,6 +286,46 @@ def test_qfused_vrows_zero_work_is_ok(lib):
     assert qfused_vrows(lib, Sq=0) == _capi.OK
 
 
+def direct_vrows(lib, **kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, o=FAKE, lse=NULL, dtype=0, B=1, Hq=4, Hkv=2, Sq=64, Sk=64, D=64,
+             qsb=4 * 64 * 64, qsh=64 * 64, qsn=64, ksb=2 * 64 * 64, ksh=64 * 64, ksn=64,
+             vsb=2 * 64 * 64, vsh=64 * 64, vsn=64, osb=4 * 64 * 64, osh=64 * 64, osn=64, causal=0, scale=0.125,
+             nsplit=1, ws=NULL, wsb=0, stream=NULL)
+    a.update(kw)
+    return lib.sage_attn_direct_fwd_vrows(*a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        (dict(dtype=1), _capi.ERR_UNSUPPORTED, "SAGE_DTYPE_F16"),
+        (dict(dtype=7), _capi.ERR_INVALID_ARG, "sage_attn_direct_fwd_vrows: dtype"),
+        (dict(D=96), _capi.ERR_UNSUPPORTED, "head_dim"),
+        (dict(v=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(k=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(v=ODD), _capi.ERR_ALIGNMENT, "q/k/value must be 16-byte aligned"),
+        (dict(vsn=60), _capi.ERR_INVALID_ARG, "V rows must not overlap"),
+        (dict(vsh=-64), _capi.ERR_INVALID_ARG, "value strides"),
+        (dict(vsn=68), _capi.ERR_ALIGNMENT, "value strides must be multiples of 16 bytes"),
+        (dict(ksn=60), _capi.ERR_INVALID_ARG, "overlap"),
+        (dict(Hq=3), _capi.ERR_INVALID_ARG, "multiple"),
+        (dict(nsplit=99), _capi.ERR_INVALID_ARG, "num_splits"),
+        # 3 key splits of 4 q-blocks (one per head, 128 rows at D = 64): 12 x 128 x 65 fp32
+        (dict(nsplit=3, Sk=1024, ksb=2 * 1024 * 64, ksh=1024 * 64, vsb=2 * 1024 * 64, vsh=1024 * 64),
+         _capi.ERR_INVALID_ARG, f"need a workspace of {4 * 3 * 128 * 65 * 4} bytes (got 0)"),
+    ],
+)
+def test_direct_vrows_validation(lib, kw, code, msg):
+    assert direct_vrows(lib, **kw) == code
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_direct_vrows_zero_work_is_ok(lib):
+    assert direct_vrows(lib, B=0) == _capi.OK
+    assert direct_vrows(lib, Sq=0) == _capi.OK
+    assert lib.sage_last_error() == b""
+
+
 def test_qfused_zero_work_is_ok(lib):
     assert qfused(lib, Sq=0) == _capi.OK
     assert qfused(lib, B=0, q=NULL) == _capi.OK

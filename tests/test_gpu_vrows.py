@@ -1,9 +1,11 @@
-"""The fused-Q INT8 attention with V read in place (sage_attn_i8_fwd_qfused_vrows, fp16 only) against the V_T
-path it replaces (v_transpose + sage_attn_i8_fwd_qfused, reference core.py:173-179,190-197): the P.V MFMAs see
+"""The fused-Q INT8 attention and the direct fp16 kernel with V read in place (sage_attn_i8_fwd_qfused_vrows,
+sage_attn_direct_fwd_vrows; fp16 only) against the V_T paths they replace (v_transpose followed by
+sage_attn_i8_fwd_qfused or sage_attn_direct_fwd, reference core.py:141-164,173-179,190-197): the P.V MFMAs see
 the same fp16 V values in the same key order, so output and LSE must match bit for bit -- at the BASELINE fp16
-configs (C2, C4 at full size), ragged and cross lengths, GQA, both layouts, a strided V view, causal and
-non-causal, unsplit and key-split plans.  Every output element starts as NaN (all must be written).  The V_T
-path itself is tied to the oracle by test_gpu_parity / test_gpu_product."""
+configs (C2, C4 at full size), the reference's cross-attention lengths (77, 154, 512 keys), ragged and cross
+lengths, GQA, both layouts, a strided V view, causal and non-causal, unsplit and key-split plans.  Every output
+element starts as NaN (all must be written).  The V_T paths themselves are tied to the oracle by
+test_gpu_parity, test_gpu_direct and test_gpu_product."""
 import pytest
 import torch
 
@@ -73,5 +75,62 @@ def test_vrows_strided_value(cfg):
     _say(f"[vrows strided V] {cfg}")
     q, k, v = (t.cuda() for t in make_inputs(cfg, seed=6))
     o_ref, lse_ref, o, lse = _run(cfg, q, k, v, 0, v_strided=True)
+    assert torch.equal(o, o_ref)
+    assert torch.equal(lse, lse_ref)
+
+
+# ------------------------------------------------------------------ the direct (fp16) kernel with V in place
+DIRECT_CASES = [
+    Config("dv_cross_q1000_kv77_d64_nhd", 1, 10, 10, 77, 64, "fp16", "NHD", False, False, Sq=1000),
+    Config("dv_cross_q700_kv154_d64", 1, 4, 4, 154, 64, "fp16", "HND", False, False, Sq=700),
+    Config("dv_2304_d64_nhd", 1, 20, 20, 2304, 64, "fp16", "NHD", False, False),
+    Config("dv_ragged1000_d128_causal_gqa", 1, 4, 2, 1000, 128, "fp16", "HND", True, False),
+    Config("dv_ragged300_d128_nhd_gqa", 2, 6, 3, 300, 128, "fp16", "NHD", False, False),
+    Config("dv_cross_q300_kv512_d128_nhd", 1, 16, 16, 512, 128, "fp16", "NHD", False, False, Sq=300),
+    Config("dv_persistent_causal_d64", 1, 8, 8, 9000, 64, "fp16", "HND", True, False),
+]
+
+
+def _run_direct(cfg, q, k, v, splits, v_strided=False):
+    from sageattention import ops
+
+    lay = ops.HND if cfg.layout == "HND" else ops.NHD
+    vt = torch.empty(cfg.B, cfg.Hkv, cfg.D, (cfg.S + 63) // 64 * 64, device="cuda", dtype=torch.float16)
+    ops.v_transpose(v, vt, lay)
+    nan = float("nan")
+    o_ref = torch.full_like(q, nan)
+    lse_ref = torch.full((cfg.B, cfg.Hq, cfg.q_len), nan, device="cuda", dtype=torch.float32)
+    ops.fp16_attn_t(q, k, vt, o_ref, lay, int(cfg.causal), cfg.D ** -0.5, 0, lse=lse_ref, num_splits=splits)
+    if v_strided:
+        wide = torch.zeros(v.shape[:-1] + (2 * cfg.D,), device="cuda", dtype=v.dtype)
+        wide[..., cfg.D // 2: cfg.D // 2 + cfg.D] = v
+        v = wide[..., cfg.D // 2: cfg.D // 2 + cfg.D]
+        assert not v.is_contiguous()
+    o = torch.full_like(q, nan)
+    lse = torch.full((cfg.B, cfg.Hq, cfg.q_len), nan, device="cuda", dtype=torch.float32)
+    ops.fp16_attn_vrows(q, k, v, o, lay, int(cfg.causal), cfg.D ** -0.5, lse=lse, num_splits=splits)
+    torch.cuda.synchronize()
+    return o_ref, lse_ref, o, lse
+
+
+@pytest.mark.parametrize("cfg", DIRECT_CASES, ids=lambda c: c.name)
+@pytest.mark.parametrize("splits", [0, 1, 3])
+def test_direct_vrows_equals_vt_path(cfg, splits):
+    """sage_attn_direct_fwd_vrows against v_transpose + sage_attn_direct_fwd (reference core.py:141-164):
+    output and LSE bit for bit, every element written."""
+    _say(f"[direct vrows] {cfg} splits={splits}")
+    q, k, v = (t.cuda() for t in make_inputs(cfg, seed=7))
+    o_ref, lse_ref, o, lse = _run_direct(cfg, q, k, v, splits)
+    assert not bool(torch.isnan(o).any()), f"{int(torch.isnan(o).sum())} output elements unwritten"
+    assert bool(torch.isfinite(lse).all()), "LSE element left unwritten"
+    assert torch.equal(o, o_ref), f"max diff {(o.float() - o_ref.float()).abs().max().item()}"
+    assert torch.equal(lse, lse_ref)
+
+
+@pytest.mark.parametrize("cfg", [DIRECT_CASES[0], DIRECT_CASES[3]], ids=lambda c: c.name)
+def test_direct_vrows_strided_value(cfg):
+    _say(f"[direct vrows strided V] {cfg}")
+    q, k, v = (t.cuda() for t in make_inputs(cfg, seed=8))
+    o_ref, lse_ref, o, lse = _run_direct(cfg, q, k, v, 0, v_strided=True)
     assert torch.equal(o, o_ref)
     assert torch.equal(lse, lse_ref)
