@@ -154,9 +154,11 @@ int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* val
 
 /*
  * Key splits of the two entry points below (non-causal launches only).  A
- * launch has B*Hq*ceil(q_len/R) q-blocks, R = 128 query rows for head_dim 64
- * (non-causal launches run two blocks per CU) and 256 otherwise (one block per
- * CU); when that leaves compute units idle
+ * launch has B*Hq*ceil(q_len/R) q-blocks, R = 128 query rows (two blocks per
+ * CU) for head_dim 64 non-causal launches and for causal launches whose
+ * 256-row q-blocks would fill at most half the CUs (except head_dim 128
+ * direct ones), and R = 256 otherwise (one block per CU); for a non-causal
+ * launch that leaves compute units idle
  * (fewer blocks than CUs, or a last round partly filled) the key range of
  * some or all blocks can be split into parts whose fp32 partial outputs and
  * log-sum-exps a second launch merges exactly

@@ -117,7 +117,7 @@ namespace w8 {
 constexpr int kBM = 256;
 constexpr int kWaves = 8;
 constexpr int kBlocksPerCu = 1;
-constexpr bool kD64NonCausalOnly = false;
+constexpr bool kSmallShape = false;
 #include "attn_body.inc"
 }  // namespace w8
 
@@ -125,12 +125,21 @@ namespace w4 {
 constexpr int kBM = 128;
 constexpr int kWaves = 4;
 constexpr int kBlocksPerCu = 2;
-constexpr bool kD64NonCausalOnly = true;
+constexpr bool kSmallShape = true;
 #include "attn_body.inc"
 }  // namespace w4
 
-// The shape a launch runs.
-bool small_blocks(int64_t head_dim, int is_causal) { return head_dim == 64 && is_causal == 0; }
+// The shape a launch runs: w4 for D = 64 non-causal launches, and for causal
+// launches whose 256-row q-blocks would fill at most half the CUs (their
+// 128-row q-blocks then fill twice as many; B1 H8 S4096 D128 INT8: -27%)
+// unless the kernel is a D = 128 direct one (its LDS fits once per CU); w8
+// for the rest (a causal launch of 256 q-blocks +4%, of 2048 +4% in w4).
+bool small_blocks(int64_t head_dim, int is_causal, bool direct, int64_t batch, int64_t q_heads, int64_t q_len) {
+  if (is_causal == 0) return head_dim == 64;
+  if (head_dim == 128 && direct) return false;
+  const int64_t qblocks = batch * q_heads * ((q_len + 255) / 256);
+  return qblocks > 0 && qblocks * 2 <= device_cus();
+}
 
 }  // namespace sage
 
@@ -172,15 +181,17 @@ void* scratch_address(const char* fn) {
 
 // attn_fwd of the block shape the launch runs (the arguments include head_dim and is_causal again)
 template <typename... Args>
-int run_attn(int64_t head_dim, int is_causal, Args... args) {
-  return small_blocks(head_dim, is_causal) ? w4::attn_fwd(args...) : w8::attn_fwd(args...);
+int run_attn(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len, int qk, Args... args) {
+  const bool direct = qk == w8::kQkF16 || qk == w8::kQkBf16 || qk == w8::kQkF16V;
+  return small_blocks(head_dim, is_causal, direct, batch, q_heads, q_len) ? w4::attn_fwd(qk, args...)
+                                                                           : w8::attn_fwd(qk, args...);
 }
 
 // The plan of the shape the launch runs and its workspace bytes (or a negative status).
 int64_t split_plan(bool quantized, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,
                    int is_causal, int num_splits, int64_t* whole, int* splits) {
   int64_t r;
-  if (small_blocks(head_dim, is_causal)) {
+  if (small_blocks(head_dim, is_causal, !quantized, batch, q_heads, q_len)) {
     w4::SplitPlan sp;
     r = w4::attn_split_plan(quantized, batch, q_heads, q_len, kv_len, head_dim, is_causal, num_splits, &sp);
     *whole = sp.nfull;
@@ -202,10 +213,10 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
                                 int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                                 int is_causal, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, w8::kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale, k_scale, out_dtype,
-                  batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim,
-                  head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h,
-                  o_stride_n, is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale,
+                  k_scale, out_dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim,
+                  q_len * head_dim, head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0,
+                  o_stride_b, o_stride_h, o_stride_n, is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd");
 }
 
 extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
@@ -215,10 +226,10 @@ extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, cons
                                     int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                                     int is_causal, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, w8::kQkI8, q_i8, k_i8, value_t, out, lse, q_scale, k_scale, out_dtype, batch,
-                  q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim, q_len * head_dim, head_dim,
-                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
-                  is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd_lse");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8, q_i8, k_i8, value_t, out, lse, q_scale,
+                  k_scale, out_dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim,
+                  q_len * head_dim, head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0,
+                  o_stride_b, o_stride_h, o_stride_n, is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd_lse");
 }
 
 extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const void* value_t, void* out, float* lse,
@@ -230,10 +241,11 @@ extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const vo
                                     int is_causal, double sm_scale, int num_splits, void* workspace,
                                     int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, dtype == SAGE_DTYPE_BF16 ? w8::kQkBf16 : w8::kQkF16, query, key, value_t,
-                  out, lse, nullptr, nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b,
-                  q_stride_h, q_stride_n, k_stride_b, k_stride_h, k_stride_n, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
-                  is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_direct_fwd");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, dtype == SAGE_DTYPE_BF16 ? w8::kQkBf16 : w8::kQkF16,
+                  query, key, value_t, out, lse, nullptr, nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len,
+                  head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b, k_stride_h, k_stride_n, 0, 0, 0,
+                  o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes,
+                  stream, "sage_attn_direct_fwd");
 }
 
 extern "C" int sage_attn_direct_fwd_vrows(const void* query, const void* key, const void* value, void* out,
@@ -246,10 +258,11 @@ extern "C" int sage_attn_direct_fwd_vrows(const void* query, const void* key, co
                                           int is_causal, double sm_scale, int num_splits, void* workspace,
                                           int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, w8::kQkF16V, query, key, value, out, lse, nullptr, nullptr, dtype, batch,
-                  q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b,
-                  k_stride_h, k_stride_n, v_stride_b, v_stride_h, v_stride_n, o_stride_b, o_stride_h, o_stride_n,
-                  is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_direct_fwd_vrows");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkF16V, query, key, value, out, lse, nullptr,
+                  nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
+                  q_stride_n, k_stride_b, k_stride_h, k_stride_n, v_stride_b, v_stride_h, v_stride_n, o_stride_b,
+                  o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream,
+                  "sage_attn_direct_fwd_vrows");
 }
 
 extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, const void* value_t, void* out,
@@ -261,10 +274,11 @@ extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, co
                                        int is_causal, double sm_scale, int num_splits, void* workspace,
                                        int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr, k_scale, dtype, batch,
-                  q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
-                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
-                  is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream, "sage_attn_i8_fwd_qfused");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
+                  k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
+                  q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b,
+                  o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream,
+                  "sage_attn_i8_fwd_qfused");
 }
 
 extern "C" int sage_attn_i8_fwd_qfused_vrows(const void* query, const int8_t* k_i8, const void* value, void* out,
@@ -277,11 +291,11 @@ extern "C" int sage_attn_i8_fwd_qfused_vrows(const void* query, const int8_t* k_
                                              int is_causal, double sm_scale, int num_splits, void* workspace,
                                              int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, w8::kQkI8FV, query, k_i8, value, out, lse, nullptr, k_scale, dtype, batch,
-                  q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
-                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, v_stride_b, v_stride_h, v_stride_n,
-                  o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes,
-                  stream, "sage_attn_i8_fwd_qfused_vrows");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8FV, query, k_i8, value, out, lse, nullptr,
+                  k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
+                  q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, v_stride_b, v_stride_h,
+                  v_stride_n, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace,
+                  workspace_bytes, stream, "sage_attn_i8_fwd_qfused_vrows");
 }
 
 extern "C" int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* k_i8, const void* value_t, void* out,
@@ -310,10 +324,11 @@ extern "C" int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* 
     ws = scratch_address(fn);
     if (ws == nullptr) return SAGE_ERR_HIP;
   }
-  return run_attn(head_dim, is_causal, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr, k_scale, dtype, batch,
-                  q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
-                  kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n,
-                  is_causal, sm_scale, num_splits, ws, ws != nullptr ? kScratchBytes : 0, stream, fn);
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
+                  k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
+                  q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b,
+                  o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, ws, ws != nullptr ? kScratchBytes : 0,
+                  stream, fn);
 }
 
 extern "C" int64_t sage_attn_workspace_bytes(int quantized, int64_t batch, int64_t q_heads, int64_t q_len,
