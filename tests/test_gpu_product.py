@@ -16,6 +16,9 @@ output element written (NaN canaries), and the reference's own benchmark shapes 
   FAIL threshold, max |out - sdpa| <= 0.05 (:216,310-317), and to cos >= 0.9999 (the band of
   benchmark_attn-result-native.txt:4,22,25,43,46,64,70,73,79,82), on sampled rows of every head against
   fp32 softmax attention cast to the output dtype, as the reference's get_sdpa_reference (:50-66).
+* ``test_reference_direct_shapes_nhd_accuracy``: the same bars at the benchmark's shapes that its dispatch sends
+  to the direct kernel (cross-attention with 77, 154 and 512 keys, short self-attention), through the fp16
+  in-place-V launch or V layout + the direct kernel as ``sageattn`` picks them.
 """
 import os
 
@@ -201,5 +204,50 @@ def test_reference_shapes_nhd_accuracy(shape):
         ref_all.append(ref)
     cs = cos_sim(np.concatenate(got_all), np.concatenate(ref_all))
     _say(f"[reference shape NHD] {name}: MaxErr {max_err:.6f} CosSim {cs:.6f} ({len(rows)} rows x {H} heads)")
+    assert max_err <= 0.05, f"{name}: MaxErr {max_err} above the reference's FAIL threshold 0.05"
+    assert cs >= 0.9999, f"{name}: CosSim {cs}"
+
+
+DIRECT_REFERENCE_SHAPES = [  # benchmark_attn/benchmark_attn.py:143-174: the shapes its dispatch sends direct
+    ("SDXL02", 1, 10, 4096, 77, 64, "fp16"),
+    ("SDXL03", 1, 10, 4096, 154, 64, "fp16"),
+    ("SDXL04", 1, 20, 1024, 1024, 64, "fp16"),
+    ("SDXL05", 1, 20, 1024, 77, 64, "fp16"),
+    ("SDXL10", 1, 20, 1536, 1536, 64, "fp16"),
+    ("SDXL16", 1, 20, 2304, 2304, 64, "fp16"),
+    ("SDXL17", 1, 20, 2304, 77, 64, "fp16"),
+    ("Anima02", 1, 16, 4096, 512, 128, "bf16"),
+]
+
+
+@pytest.mark.parametrize("shape", DIRECT_REFERENCE_SHAPES, ids=lambda s: s[0])
+def test_reference_direct_shapes_nhd_accuracy(shape):
+    """The reference benchmark's direct-path shapes (cross-attention with 77 / 154 / 512 keys, short
+    self-attention), called as it calls them (NHD), through ``sageattn``: fp16 ones up to 1280 keys (D = 64)
+    run the one launch that reads V in place, the others V layout + the direct kernel.  Held to the
+    benchmark's FAIL threshold (MaxErr <= 0.05 against fp32 softmax attention cast to the output dtype) and
+    cos >= 0.9999, on sampled rows of every head."""
+    from sageattention import sageattn
+    from sageattention.core import use_direct_path
+
+    name, B, H, Sq, Sk, D, dt = shape
+    assert use_direct_path(D, Sq, Sk, False, "NHD"), "the reference's NHD dispatch sends this shape direct"
+    cfg = Config(name, B, H, H, Sk, D, dt, "NHD", False, False, Sq=Sq)
+    q, k, v = make_inputs(cfg, seed=0)
+    o = sageattn(q.cuda(), k.cuda(), v.cuda(), tensor_layout="NHD", is_causal=False)
+    torch.cuda.synchronize()
+    og = orc.to_hnd(np_to_f32(to_np(o), dt), "NHD")
+    qh, kh, vh = (orc.to_hnd(np_to_f32(to_np(t), dt), "NHD") for t in (q, k, v))
+    rows = sample_rows(Sq, 24, np.random.default_rng(3))
+    max_err, got_all, ref_all = 0.0, [], []
+    for h in range(H):
+        ref = sdpa_rows_fp32(qh[0, h], kh[0, h], vh[0, h], rows, False, D ** -0.5)
+        ref = np_to_f32(orc.from_f32(ref.astype(np.float32), dt), dt)
+        got = og[0, h, rows]
+        max_err = max(max_err, float(np.max(np.abs(got.astype(np.float64) - ref))))
+        got_all.append(got)
+        ref_all.append(ref)
+    cs = cos_sim(np.concatenate(got_all), np.concatenate(ref_all))
+    _say(f"[reference shape NHD, direct] {name}: MaxErr {max_err:.6f} CosSim {cs:.6f} ({len(rows)} rows x {H} heads)")
     assert max_err <= 0.05, f"{name}: MaxErr {max_err} above the reference's FAIL threshold 0.05"
     assert cs >= 0.9999, f"{name}: CosSim {cs}"
