@@ -95,12 +95,14 @@ int device_cus() {
 //     waves do not share barriers, so one block's prologue, epilogue and
 //     barrier waits overlap the other's key loop; each block loads its own K/V
 //     tiles (twice the L2->LDS traffic of w8).
-// w4 runs the D = 64 non-causal launches (direct and INT8), w8 all others.
-// Same-box timings against w8 (identical outputs): D = 64 non-causal -7% to
-// -27% (the direct kernel at B1 H20 S1024: 21.3 -> 15.6 us; INT8 at B1 H10
-// S4096: 65.9 -> 56.2 us); causal launches +3% to +6% and D = 128 non-causal
-// launches with key splits +3% to +4% (the doubled tile traffic), so those
-// stay on w8.  The D = 128 direct kernel's 98 KB of LDS would not fit twice.
+// w4 runs the D = 64 non-causal launches (direct and INT8) and the causal
+// launches with few q-blocks (small_blocks), w8 all others.  Same-box timings
+// against w8 (identical outputs): D = 64 non-causal -7% to -27% (the direct
+// kernel at B1 H20 S1024: 21.3 -> 15.6 us; INT8 at B1 H10 S4096: 65.9 -> 56.2
+// us); causal launches of one or more full rounds +2% to +6% and D = 128
+// non-causal launches with key splits +3% to +4% (the doubled tile traffic),
+// so those stay on w8.  The D = 128 direct kernel's 98 KB of LDS would not fit
+// twice.
 // The stamps build (build.py --stamps, SAGE_STAMPS=1) adds per-wave cycle
 // stamps to the attention kernels (attn_body.inc, StampField) and the two
 // functions below that read them; the default build has neither.
