@@ -101,8 +101,8 @@ int device_cus() {
 // kernel at B1 H20 S1024: 21.3 -> 15.6 us; INT8 at B1 H10 S4096: 65.9 -> 56.2
 // us); causal launches of one or more full rounds +2% to +6% and D = 128
 // non-causal launches with key splits +3% to +4% (the doubled tile traffic),
-// so those stay on w8.  The D = 128 direct kernel's 98 KB of LDS would not fit
-// twice.
+// so those stay on w8.  The D = 128 direct kernel's 98 KB of LDS fits once per
+// CU: its w4 launches (causal, few q-blocks) run one block per CU.
 // The stamps build (build.py --stamps, SAGE_STAMPS=1) adds per-wave cycle
 // stamps to the attention kernels (attn_body.inc, StampField) and the two
 // functions below that read them; the default build has neither.
@@ -133,12 +133,13 @@ constexpr bool kSmallShape = true;
 
 // The shape a launch runs: w4 for D = 64 non-causal launches, and for causal
 // launches whose 256-row q-blocks would fill at most half the CUs (their
-// 128-row q-blocks then fill twice as many; B1 H8 S4096 D128 INT8: -27%)
-// unless the kernel is a D = 128 direct one (its LDS fits once per CU); w8
-// for the rest (a causal launch of 256 q-blocks +4%, of 2048 +4% in w4).
-bool small_blocks(int64_t head_dim, int is_causal, bool direct, int64_t batch, int64_t q_heads, int64_t q_len) {
+// 128-row q-blocks then fill twice as many, one block per CU; B1 H8 S4096
+// D128 INT8: -27%; the D = 128 direct kernel, whose 98 KB of LDS fits once per
+// CU, at B1 H8/H16 S1024-2048: -27% to -32%); w8 for the rest (a causal launch
+// of 256 q-blocks +4%, of 2048 +4% in w4; the D = 128 direct one of 256
+// q-blocks +9%).
+bool small_blocks(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len) {
   if (is_causal == 0) return head_dim == 64;
-  if (head_dim == 128 && direct) return false;
   const int64_t qblocks = batch * q_heads * ((q_len + 255) / 256);
   return qblocks > 0 && qblocks * 2 <= device_cus();
 }
@@ -184,16 +185,15 @@ void* scratch_address(const char* fn) {
 // attn_fwd of the block shape the launch runs (the arguments include head_dim and is_causal again)
 template <typename... Args>
 int run_attn(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len, int qk, Args... args) {
-  const bool direct = qk == w8::kQkF16 || qk == w8::kQkBf16 || qk == w8::kQkF16V;
-  return small_blocks(head_dim, is_causal, direct, batch, q_heads, q_len) ? w4::attn_fwd(qk, args...)
-                                                                           : w8::attn_fwd(qk, args...);
+  return small_blocks(head_dim, is_causal, batch, q_heads, q_len) ? w4::attn_fwd(qk, args...)
+                                                                   : w8::attn_fwd(qk, args...);
 }
 
 // The plan of the shape the launch runs and its workspace bytes (or a negative status).
 int64_t split_plan(bool quantized, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,
                    int is_causal, int num_splits, int64_t* whole, int* splits) {
   int64_t r;
-  if (small_blocks(head_dim, is_causal, !quantized, batch, q_heads, q_len)) {
+  if (small_blocks(head_dim, is_causal, batch, q_heads, q_len)) {
     w4::SplitPlan sp;
     r = w4::attn_split_plan(quantized, batch, q_heads, q_len, kv_len, head_dim, is_causal, num_splits, &sp);
     *whole = sp.nfull;

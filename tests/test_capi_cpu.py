@@ -388,7 +388,7 @@ def test_split_plan(lib):
     assert plan(False, 1, 4, 600, 128, 64, False, 9) == (0, 2)      # at most one split per key tile
     # causal: whole; 12 q-blocks of 256 rows fill at most half the CUs, so 20 of 128 rows run instead
     assert plan(True, 1, 4, 600, 4096, 128, True, 4) == (20, 1)
-    assert plan(False, 1, 4, 600, 4096, 128, True, 4) == (12, 1)    # not the D = 128 direct kernel
+    assert plan(False, 1, 4, 600, 4096, 128, True, 4) == (20, 1)    # the D = 128 direct kernel too
     assert plan(True, 1, 64, 600, 4096, 128, True, 0) == (192, 1)   # 192 q-blocks of 256 rows: more than half
     assert plan(True, 1, 4, 600, 4096, 128, False, 1) == (12, 1)
     assert plan(True, 1, 4, 600, 0, 128, False, 0) == (12, 1)       # no keys
