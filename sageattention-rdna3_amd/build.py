@@ -6,7 +6,7 @@ Cross-compiles for gfx950 with hipcc; no GPU is needed.  Every call recompiles.
 ``--asan`` builds the host-AddressSanitizer variant of the library instead
 (``_build_asan/``, for the C-ABI tests on the CPU); ``--stamps`` the variant
 whose attention kernels record per-wave cycle stamps (``_build_stamps/``, read
-by ``stamps.py``).
+through ``sage_stamps_read``).
 
 Flags:
   * ``-Xclang -target-feature -Xclang -packed-fp32-ops`` on every device
@@ -165,7 +165,7 @@ def build_asan(verbose: bool = False) -> str:
 
 # Cycle-stamps build of the library: the attention kernels compiled with SAGE_STAMPS=1 (per-wave s_memtime
 # counts of item phases and key-loop steps, csrc/attn_body.inc) plus sage_stamps_read / sage_stamps_clear.
-# Loaded through SAGEATTN_MI355X_LIB by stamps.py; never the product library.
+# Loaded through SAGEATTN_MI355X_LIB by a measurement script; never the product library.
 STAMPS_DIR = os.path.join(HERE, "_build_stamps")
 STAMPS_LIB = os.path.join(STAMPS_DIR, "libsage_mi355x_stamps.so")
 
