@@ -68,27 +68,30 @@ OUTLIER_FRAC = {"C5": 0.01}
 
 
 def make_inputs(cfg, device, name=None):
+    """q, k, v of the config, generated on the CPU in fp32 from torch.Generator().manual_seed(0) (q, k, v in
+    that order, then C3's K offset and C5's outlier channels), cast to the config's dtype and copied to
+    ``device`` before any timing: the same bits as the parity tests' inputs for that seed."""
     import torch
 
     B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
     dtype = torch.bfloat16 if dt == "bf16" else torch.float16
-    g = torch.Generator(device=device).manual_seed(0)
+    g = torch.Generator().manual_seed(0)
 
     def shp(h):
         return (B, h, S, D) if layout == "HND" else (B, S, h, D)
 
-    q = torch.randn(shp(Hq), generator=g, device=device, dtype=torch.float32)
-    k = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32)
-    v = torch.randn(shp(Hkv), generator=g, device=device, dtype=torch.float32)
+    q = torch.randn(shp(Hq), generator=g)
+    k = torch.randn(shp(Hkv), generator=g)
+    v = torch.randn(shp(Hkv), generator=g)
     if name in K_OFFSET_STD:
-        off = torch.randn((B, Hkv, 1, D), generator=g, device=device) * K_OFFSET_STD[name]
+        off = torch.randn((B, Hkv, 1, D), generator=g) * K_OFFSET_STD[name]
         k += off if layout == "HND" else off.transpose(1, 2)
     if name in OUTLIER_FRAC:
         n_out = max(1, round(OUTLIER_FRAC[name] * D))
-        chans = torch.randperm(D, generator=g, device=device)[:n_out]
+        chans = torch.randperm(D, generator=g)[:n_out]
         q[..., chans] *= 20.0
         k[..., chans] *= 20.0
-    return q.to(dtype), k.to(dtype), v.to(dtype)
+    return tuple(t.to(dtype).to(device) for t in (q, k, v))
 
 
 class SclkSampler:
@@ -198,6 +201,52 @@ def timed_launches(fn, n, stream, dev, queue=True):
     return e0.elapsed_time(e1) / n
 
 
+def step_breakdown(cfg, q, k, v, n, stream):
+    """The launches of one ``sageattn`` INT8 step -- the K prologue (smooth_k: the K mean's chunk sums, then K
+    quantisation finishing the mean + V layout; else K quantisation + V layout in one launch), then the
+    attention kernel that quantises Q (and the key-split merge when its plan splits) -- issued through the ops
+    layer in the same order on the same tensors, n steps back to back with HIP events on the launch stream
+    between them: each part's time inside the step, and the time the GPU waits between steps (host issue)."""
+    import torch
+
+    from sageattention import ops
+
+    B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
+    lay = ops.HND if layout == "HND" else ops.NHD
+    empty = torch.empty(0, device=q.device, dtype=q.dtype)
+
+    def one(ev):
+        if ev is not None:
+            ev[0].record(stream)
+        if smooth:
+            k8, ks, vt = ops.prep_kv_int8_smooth(k, v, lay)
+        else:
+            k8, ks, vt = ops.prep_kv_int8(k, v, empty, lay)
+        if ev is not None:
+            ev[1].record(stream)
+        o = torch.empty_like(q)
+        ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5)
+        if ev is not None:
+            ev[2].record(stream)
+        return o
+
+    for _ in range(3):
+        one(None)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
+    t0 = time.perf_counter()
+    for e in evs:
+        one(e)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / n
+    prep = sum(e[0].elapsed_time(e[1]) for e in evs) / n
+    attn = sum(e[1].elapsed_time(e[2]) for e in evs) / n
+    gap = sum(evs[i][2].elapsed_time(evs[i + 1][0]) for i in range(n - 1)) / max(1, n - 1)
+    return {"steps": n, "prologue_us": round(prep * 1e3, 2), "attention_ms": round(attn, 5),
+            "gap_between_steps_us": round(gap * 1e3, 2), "sum_ms": round(prep + attn + gap, 5),
+            "ms_per_step_instrumented": round(wall, 5)}
+
+
 def cpu_baseline(cfg, budget_s):
     """The PyTorch CPU implementation of the same quantized math (oracle/torch_cpu.py: per-block INT8 Q/K
     quantisation with fp32 scales, K mean for smooth_k, fp16 V, exact integer QK^T, fp32 online softmax over
@@ -256,8 +305,10 @@ def kernels_only(cfg, q, k, v, n):
     B, Hq, Hkv, S, D, dt, layout, causal, smooth = cfg
     lay = ops.HND if layout == "HND" else ops.NHD
     for _ in range(n):
-        mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=q.device, dtype=q.dtype)
-        k8, ks, vt = ops.prep_kv_int8(k, v, mean, lay)
+        if smooth:
+            k8, ks, vt = ops.prep_kv_int8_smooth(k, v, lay)
+        else:
+            k8, ks, vt = ops.prep_kv_int8(k, v, torch.empty(0, device=q.device, dtype=q.dtype), lay)
         o = torch.empty_like(q)
         ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5)
     dq, dk, dv = make_inputs(DIRECT_CFG, q.device)
@@ -406,10 +457,10 @@ def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
             if names is not None and name not in names:
                 continue
             dtype = torch.bfloat16 if dt == "bf16" else torch.float16
-            g = torch.Generator(device=dev).manual_seed(0)
-            q = torch.randn((B, Sq, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-            k = torch.randn((B, Sk, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
-            v = torch.randn((B, Sk, H, D), generator=g, device=dev, dtype=torch.float32).to(dtype)
+            g = torch.Generator().manual_seed(0)
+            q = torch.randn((B, Sq, H, D), generator=g).to(dtype).to(dev)
+            k = torch.randn((B, Sk, H, D), generator=g).to(dtype).to(dev)
+            v = torch.randn((B, Sk, H, D), generator=g).to(dtype).to(dev)
             direct = use_direct_path(D, Sq, Sk, False, "NHD")
             calls = n if Sq * Sk >= 1 << 24 else max(n, 200)  # enough calls to time the short shapes
             times = {mode: [] for mode in modes}
@@ -481,6 +532,7 @@ def config_probe(name, dev, n):
 
     ms_step = timed(lambda: sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth), n,
                     queue=False)
+    bd = step_breakdown(cfg, q, k, v, n, stream)
     mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=dev, dtype=q.dtype)
     k8, ks, vt = ops.prep_kv_int8(k, v, mean, lay)
     o = torch.empty_like(q)
@@ -502,6 +554,8 @@ def config_probe(name, dev, n):
     ms_prep = timed(rotated(lambda i: outs.__setitem__(i, ops.prep_kv_int8(kr[i], vr[i], mean, lay))), n)
     ms_kq = timed(rotated(lambda i: outs.__setitem__(i, ops.quant_k_int8(kr[i], mean, lay))), n)
     ms_mean = timed(rotated(lambda i: ops.mean_seq(kr[i], lay)), n) if smooth else None
+    ms_smooth = timed(rotated(lambda i: outs.__setitem__(i, ops.prep_kv_int8_smooth(kr[i], vr[i], lay))), n) \
+        if smooth else None
     del kr, vr, outs
     ops_step = attn_ops(B, Hq, S, S, D, causal)
     nk = B * Hkv * S * D
@@ -534,11 +588,19 @@ def config_probe(name, dev, n):
         "k_mean_us": round(ms_mean * 1e3, 2) if smooth else None,
         "k_mean_GBps": round(mean_bytes / ms_mean / 1e6, 1) if smooth else None,
         "k_mean_frac_hbm": round(mean_bytes / ms_mean / 1e6 / PEAK_HBM_GBS, 4) if smooth else None,
+        # smooth_k: the prologue sageattn runs (K mean's chunk sums, then K quantisation finishing the mean + V
+        # layout), against the HBM bytes of the K mean read plus prep_kv's
+        "prep_kv_smooth_us": round(ms_smooth * 1e3, 2) if smooth else None,
+        "prep_kv_smooth_frac_hbm": round((mean_bytes + kq_bytes + vl_bytes) / ms_smooth / 1e6 / PEAK_HBM_GBS, 4)
+        if smooth else None,
+        "step_breakdown": dict(bd, unaccounted_us=round((ms_step - bd["sum_ms"]) * 1e3, 2)),
     }
     log(f"[bench] {name}: step {ms_step:.4f} ms ({r['effective_tops']} TOPS), attention {ms_attn:.4f} ms "
         f"({100 * r['attn_frac_int8_peak']:.1f}% INT8 peak), prep_kv {r['prep_kv_us']} us "
         f"({100 * r['prep_kv_frac_hbm']:.1f}% HBM; a copy of the same bytes {r['copy_same_bytes_us']} us = "
-        f"{r['copy_same_bytes_GBps']} GB/s), K quant {r['k_quant_us']} us, K mean {r['k_mean_us']} us")
+        f"{r['copy_same_bytes_GBps']} GB/s), K quant {r['k_quant_us']} us, K mean {r['k_mean_us']} us, smooth_k "
+        f"prologue {r['prep_kv_smooth_us']} us; in-step prologue {bd['prologue_us']} us + attention "
+        f"{bd['attention_ms']:.4f} ms + gap {bd['gap_between_steps_us']} us")
     del q, k, v, o, k8, ks, vt
     torch.cuda.empty_cache()
     return r
@@ -626,9 +688,17 @@ def main():
     log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS; shader clock during the "
         f"steps (sysfs) {sampler.mhz()} MHz ({sampler.kind or 'not readable'}, {len(sampler.samples)} samples)")
 
-    # ---- per-kernel timing with HIP events on the launch stream
+    # ---- the same steps' launches with HIP events between them (in-step kernel times)
     lay = ops.HND if layout == "HND" else ops.NHD
     stream = torch.cuda.current_stream(dev)
+    bd = step_breakdown(cfg, q, k, v, args.steps, stream)
+    bd["ms_per_step"] = round(ms_step, 5)
+    bd["unaccounted_us"] = round((ms_step - bd["sum_ms"]) * 1e3, 2)
+    log(f"[bench] in-step: prologue {bd['prologue_us']} us + attention {bd['attention_ms']:.4f} ms + gap "
+        f"{bd['gap_between_steps_us']} us = {bd['sum_ms']:.4f} ms (instrumented steps {bd['ms_per_step_instrumented']:.4f} "
+        f"ms, sageattn steps {ms_step:.4f} ms)")
+
+    # ---- per-kernel timing with HIP events on the launch stream, back to back
     mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=dev, dtype=q.dtype)
     q8, qs, k8, ks = ops.quant_qk_int8(q, k, mean, lay, D ** -0.5)
     vt = torch.empty(B, Hkv, D, (S + 63) // 64 * 64, device=dev, dtype=torch.float16)
@@ -669,16 +739,21 @@ def main():
     ms_prep = timed(rotated(lambda i: qouts.__setitem__(i, ops.prep_kv_int8(kr[i], vr[i], mean, lay))), n_k)
     ms_vl = timed(rotated(lambda i: ops.v_transpose(vr[i], vtr[i], lay)), n_k)
     ms_mean = timed(rotated(lambda i: ops.mean_seq(kr[i], lay)), n_k) if smooth else 0.0
+    ms_prep_smooth = (timed(rotated(lambda i: qouts.__setitem__(i, ops.prep_kv_int8_smooth(kr[i], vr[i], lay))), n_k)
+                      if smooth else None)
     del qr, kr, vr, vtr, qouts
     torch.cuda.synchronize()
-    achieved = ops_step / (ms_attn * 1e-3) / 1e12
+    # the roofline's kernel time: the attention kernel inside the steps (what ms_per_step contains)
+    achieved = ops_step / (bd["attention_ms"] * 1e-3) / 1e12
+    achieved_b2b = ops_step / (ms_attn * 1e-3) / 1e12
     nq, nk = B * Hq * S * D, B * Hkv * S * D
     quant_bytes = 2 * (nq + nk) + (nq + nk) + 4 * (B * Hq * ((S + 31) // 32) + B * Hkv * ((S + 15) // 16))
     kquant_bytes = 2 * nk + nk + 4 * B * Hkv * ((S + 15) // 16)
     vl_bytes = 2 * nk + 2 * B * Hkv * D * ((S + 63) // 64 * 64)
     mean_bytes = 2 * nk + 2 * B * Hkv * D
     mixed = 2.0 / (1.0 / PEAK_INT8_TOPS + 1.0 / PEAK_F16_TFLOPS)
-    log(f"[bench] attn kernel {ms_attn:.4f} ms = {achieved:.1f} TOPS ({100 * achieved / PEAK_INT8_TOPS:.1f}% INT8 peak); "
+    log(f"[bench] attn kernel in the steps {bd['attention_ms']:.4f} ms = {achieved:.1f} TOPS "
+        f"({100 * achieved / PEAK_INT8_TOPS:.1f}% INT8 peak), back to back {ms_attn:.4f} ms; "
         f"(two-kernel path {ms_attn_unfused:.4f} ms); quant Q+K {ms_quant * 1e3:.1f} us = "
         f"{quant_bytes / ms_quant / 1e6:.0f} GB/s, K only {ms_kquant * 1e3:.1f} us; "
         f"v_layout {ms_vl * 1e3:.1f} us = {vl_bytes / ms_vl / 1e6:.0f} GB/s; K quant + V layout in one launch "
@@ -693,11 +768,17 @@ def main():
         configs = {name: config_probe(name, dev, n_k) for name in args.configs.split(",") if name}
     ref_shapes = None if args.no_probes or "reference" in skip else reference_shapes_probe(dev, n_k)
 
+    # HBM bytes per attention launch: not measured in this run (counters need their own rocprofv3 --pmc
+    # runs); the figure of the committed profile of this workload, labelled as such
     traffic = None
+    traffic_source = None
     tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")
     if os.path.exists(tfile):
         with open(tfile) as f:
             traffic = json.load(f).get("attn_bytes_per_launch")
+        traffic_source = (f"profiles/hbm_traffic_{args.config}.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of "
+                          f"bench.py --kernels-only, each scaled by the same counter on a 1 GiB device copy "
+                          f"(committed profile, not measured in this run)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -717,8 +798,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic N(0,1) inputs generated on the GPU from seed 0 (C3: K plus a per-channel offset of std 2; "
-                "C5: 1% of the channels of Q and K x20)",
+        "data": "synthetic N(0,1) inputs generated on the CPU from torch.Generator().manual_seed(0) in fp32, cast "
+                "and copied to the GPU before timing (C3: K plus a per-channel offset of std 2; C5: 1% of the "
+                "channels of Q and K x20)",
         "config": {
             "workload": f"{args.config}: sageattn B{B} Hq{Hq} Hkv{Hkv} S{S} D{D} {dt} {layout} "
                         f"{'causal' if causal else 'non-causal'} smooth_k={smooth}",
@@ -733,8 +815,12 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_INT8_TOPS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel": "attn_fwd_kernel (int8 QK, Q quantised in the kernel)",
-            "kernel_ms": round(ms_attn, 5),
+            "kernel_ms": bd["attention_ms"],
+            "kernel_ms_source": "HIP events around the attention launch inside the steps (step_breakdown)",
+            "kernel_ms_back_to_back": round(ms_attn, 5),
+            "frac_back_to_back": round(achieved_b2b / PEAK_INT8_TOPS, 4),
             "two_kernel_path_attn_ms": round(ms_attn_unfused, 5),
             "frac_of_mixed_int8_fp16_ceiling": round(achieved / mixed, 4),
         },
@@ -751,7 +837,9 @@ def main():
             "v_layout_GBps": round(vl_bytes / ms_vl / 1e6, 1),
             "k_mean_us": round(ms_mean * 1e3, 2) if smooth else None,
             "k_mean_GBps": round(mean_bytes / ms_mean / 1e6, 1) if smooth else None,
+            "prep_kv_smooth_us": round(ms_prep_smooth * 1e3, 2) if smooth else None,
         },
+        "step_breakdown": bd,
         "direct": direct,
         "configs": configs,
         "reference_shapes": ref_shapes,

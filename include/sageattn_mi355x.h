@@ -119,6 +119,26 @@ int sage_prep_kv_i8(const void* key, const void* value, const void* key_mean, in
                     int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n, void* stream);
 
 /*
+ * sage_k_mean followed by sage_prep_kv_i8 with that mean (smooth_k), in two
+ * launches instead of three: the K mean's chunk sums (into `workspace`, which
+ * holds sage_k_mean_workspace_bytes() bytes, no initialisation), then one
+ * launch in which the K-quantisation blocks finish the mean themselves (the
+ * same additions in the same order as sage_k_mean, so the same mean bit for
+ * bit) and quantise K minus it, beside the V layout blocks.  Outputs equal
+ * sage_k_mean + sage_prep_kv_i8 bit for bit: k_i8, k_scale, value_t as there,
+ * and key_mean [B,Hkv,D] contiguous of `dtype` (2-byte aligned; NULL = not
+ * written).  Calls sharing one workspace on different streams race.
+ * No single reference counterpart: mean_seq (csrc/attn_gfx11.cu:1937-1972,
+ * kernel :94-145) and the K half of quant_qk_int8 (:1974-2067) with
+ * v_transpose (:1889-1935), as sageattention/core.py:173-193 calls them.
+ */
+int sage_prep_kv_i8_smooth(const void* key, const void* value, void* key_mean, void* workspace, int8_t* k_i8,
+                           float* k_scale, void* value_t, int dtype, int64_t batch, int64_t kv_heads,
+                           int64_t kv_len, int64_t head_dim, int64_t k_stride_b, int64_t k_stride_h,
+                           int64_t k_stride_n, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n,
+                           void* stream);
+
+/*
  * Fused attention: S = (q_i8 . k_i8) * q_scale * k_scale (log2 domain), causal
  * mask top-left (key j > query i masked), online softmax with exp2, P rounded
  * to fp16, O = P . V_T (fp32 accumulation), out = O / rowsum cast to out_dtype.
@@ -154,10 +174,11 @@ int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* val
 
 /*
  * Key splits of the two entry points below (non-causal launches only).  A
- * launch has B*Hq*ceil(q_len/R) q-blocks, R = 128 query rows (two blocks per
- * CU) for head_dim 64 non-causal launches and for causal launches whose
- * 256-row q-blocks would fill at most half the CUs (except head_dim 128
- * direct ones), and R = 256 otherwise (one block per CU); for a non-causal
+ * launch has B*Hq*ceil(q_len/R) q-blocks, R = 128 query rows for head_dim 64
+ * non-causal launches and for causal launches (every kind) whose 256-row
+ * q-blocks would fill at most half the CUs, and R = 256 otherwise (one block
+ * per CU).  128-row blocks run two per CU, except the head_dim 128 direct
+ * kernel's, whose LDS fits once per CU; for a non-causal
  * launch that leaves compute units idle
  * (fewer blocks than CUs, or a last round partly filled) the key range of
  * some or all blocks can be split into parts whose fp32 partial outputs and
@@ -244,15 +265,17 @@ int sage_attn_i8_fwd_qfused_vrows(const void* query, const int8_t* k_i8, const v
  * sage_attn_i8_fwd_qfused without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The key
- * splits' partial outputs go to a scratch array of 32 MiB that the library
+ * splits' partial outputs go to a scratch array of 64 MiB that the library
  * holds in each GPU's memory until the process ends; the call allocates
- * nothing.  num_splits 0 picks the best plan whose partials fit the scratch;
- * a forced n > 1 whose partials would not fit fails with SAGE_ERR_UNSUPPORTED.
+ * nothing.  A forced n > 1 whose partials would not fit fails with
+ * SAGE_ERR_UNSUPPORTED.  num_splits 0 runs the plan sage_attn_i8_fwd_qfused
+ * would choose (sage_attn_split_plan) when its partials fit the scratch, and
+ * otherwise the best plan that fits, whose result differs by rounding only.
  * Every call on one GPU shares that GPU's scratch: calls that overlap on one
  * GPU (different streams, or host threads) race on it; calls ordered on one
  * stream do not.  The first call that may split, per device, looks the
  * scratch's address up (with that device current).  Results equal those of
- * sage_attn_i8_fwd_qfused with the same num_splits.
+ * sage_attn_i8_fwd_qfused with the same num_splits whenever the plans agree.
  */
 int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* k_i8, const void* value_t, void* out,
                                     float* lse, const float* k_scale, int dtype,

@@ -47,7 +47,7 @@ reduction with hardware exp2; it is compared within a stated tolerance.
 The K-mean summation order (parity pinned only through closed forms and fp64
 bounds, since the reference's own order is not reproducible: it was compiled
 with -ffast-math, ``setup.py:183``):
-    rows are cut into chunks of 256; inside a chunk, lane slot r (0..R-1,
+    rows are cut into chunks of 1024; inside a chunk, lane slot r (0..R-1,
     R = 256 / (D/8)) sums rows r, r+R, r+2R, ... in increasing order; the R slot
     sums are added in increasing r; the chunk sums are added in increasing
     chunk order; the total is divided by fp32(S) and rounded to the dtype.
@@ -69,7 +69,7 @@ Q_GROUP = 32  # csrc/attn_gfx11.cu:46 (MIN_BLK_Q)
 K_GROUP = 16  # csrc/attn_gfx11.cu:47 (MIN_BLK_K)
 AMAX_FLOOR = np.float32(1e-7)  # csrc/attn_gfx11.cu:192
 VT_ALIGN = 64  # sageattention/core.py:174 (ceil64 padding of V_T)
-MEAN_CHUNK = 256  # this build's K-mean chunk (rows per partial sum)
+MEAN_CHUNK = 1024  # this build's K-mean chunk (rows per partial sum)
 
 _f32 = np.float32
 
@@ -208,7 +208,7 @@ def quant_qk_int8(q, k, dtype, layout, sm_scale, k_mean=None):
 # K mean (smooth_k)
 # --------------------------------------------------------------------------
 def mean_slots(head_dim: int) -> int:
-    """Number of row slots per 256-row chunk: 256 / (head_dim / 8)."""
+    """Number of row slots of a chunk (one per 16-byte column piece of 256 threads): 256 / (head_dim / 8)."""
     return 256 // (head_dim // 8)
 
 

@@ -156,26 +156,29 @@ py::object sageattn_fwd(at::Tensor q, at::Tensor k, at::Tensor v, int64_t layout
                                  static_cast<int>(num_splits), ptr(ws), ws_bytes, stream));
     }
   } else {
-    // K mean for smooth_k (reference mean_seq, csrc/attn_gfx11.cu:1937-1972)
-    at::Tensor k_mean;
-    if (smooth_k && Sk > 0) {
-      k_mean = at::empty({B, Hkv, D}, k.options());
-      const int64_t mb = sage_k_mean_workspace_bytes(B, Hkv, Sk, D);
-      if (mb < 0) check("sage_k_mean_workspace_bytes", static_cast<int>(mb));
-      at::Tensor mws = at::empty({(std::max<int64_t>(mb, 4) + 3) / 4}, q.options().dtype(at::kFloat));
-      check("sage_k_mean", sage_k_mean(k.data_ptr(), k_mean.data_ptr(), mws.data_ptr(), dtype, B, Hkv, Sk, D, kd.sb,
-                                       kd.sh, kd.sn, stream));
-    }
     // K quantisation and the V transform in one launch; Q is quantised inside
     // the attention kernel (the q_int8 and q_scale of quant_qk_int8, so the
-    // same output, without the int8 Q round trip)
+    // same output, without the int8 Q round trip).  smooth_k: K minus its mean
+    // (reference mean_seq, csrc/attn_gfx11.cu:1937-1972), the mean's chunk
+    // sums in a launch before, finished by the quantisation blocks
     at::Tensor k8 = at::empty({B, Hkv, Sk, D}, q.options().dtype(at::kChar));
     at::Tensor ks = at::empty({B, Hkv, (Sk + SAGE_K_GROUP - 1) / SAGE_K_GROUP}, q.options().dtype(at::kFloat));
     at::Tensor vt = at::empty({B, Hkv, D, np}, q.options().dtype(at::kHalf));
-    check("sage_prep_kv_i8",
-          sage_prep_kv_i8(k.data_ptr(), v.data_ptr(), ptr(k_mean), static_cast<int8_t*>(k8.data_ptr()),
-                          static_cast<float*>(ks.data_ptr()), vt.data_ptr(), dtype, B, Hkv, Sk, D, kd.sb, kd.sh,
-                          kd.sn, vd.sb, vd.sh, vd.sn, stream));
+    if (smooth_k && Sk > 0) {
+      const int64_t mb = sage_k_mean_workspace_bytes(B, Hkv, Sk, D);
+      if (mb < 0) check("sage_k_mean_workspace_bytes", static_cast<int>(mb));
+      at::Tensor mws = at::empty({(std::max<int64_t>(mb, 4) + 3) / 4}, q.options().dtype(at::kFloat));
+      check("sage_prep_kv_i8_smooth",
+            sage_prep_kv_i8_smooth(k.data_ptr(), v.data_ptr(), nullptr, mws.data_ptr(),
+                                   static_cast<int8_t*>(k8.data_ptr()), static_cast<float*>(ks.data_ptr()),
+                                   vt.data_ptr(), dtype, B, Hkv, Sk, D, kd.sb, kd.sh, kd.sn, vd.sb, vd.sh, vd.sn,
+                                   stream));
+    } else {
+      check("sage_prep_kv_i8",
+            sage_prep_kv_i8(k.data_ptr(), v.data_ptr(), nullptr, static_cast<int8_t*>(k8.data_ptr()),
+                            static_cast<float*>(ks.data_ptr()), vt.data_ptr(), dtype, B, Hkv, Sk, D, kd.sb, kd.sh,
+                            kd.sn, vd.sb, vd.sh, vd.sn, stream));
+    }
     // return_lse: the reference returns a zero placeholder (core.py:203-211);
     // the fused kernel writes the real log-sum-exp of each row
     int64_t ws_bytes = 0;

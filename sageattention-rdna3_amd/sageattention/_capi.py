@@ -50,6 +50,8 @@ SIGNATURES = {
                               ctypes.c_double, _P]),
     "sage_prep_kv_i8": (_I, [_P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64,
                              _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "sage_prep_kv_i8_smooth": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I64, _I64, _I64, _I64,
+                                    _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "sage_v_layout_padded_len": (_I64, [_I64]),
     "sage_v_layout": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
     "sage_attn_i8_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I,

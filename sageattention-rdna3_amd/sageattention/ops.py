@@ -164,6 +164,31 @@ def _prep_kv_launch(key, value, key_mean, B, Hkv, Sk, D, kst, vst, stream) -> Li
     return [k8, ks, vt]
 
 
+def prep_kv_int8_smooth(key: torch.Tensor, value: torch.Tensor, tensor_layout: int,
+                        return_mean: bool = False) -> List[torch.Tensor]:
+    """:func:`mean_seq` + :func:`prep_kv_int8` (K smoothed by its mean) in two launches instead of
+    three -> [k_int8, k_scale, value_t] (+ key_mean with ``return_mean``), the same tensors bit for
+    bit (this build's fusion of the reference's mean_seq, csrc/attn_gfx11.cu:1937-1972, with the K
+    half of quant_qk_int8 and v_transpose; sageattention/core.py:186-193)."""
+    (B, Hkv, Sk, D), kst = _bhnd(key, tensor_layout)
+    (Bv, Hv, Sv, Dv), vst = _bhnd(value, tensor_layout)
+    if (Bv, Hv, Sv, Dv) != (B, Hkv, Sk, D) or value.dtype != key.dtype:
+        raise ValueError("key and value must have the same shape and dtype")
+    dev = key.device
+    k8 = torch.empty((B, Hkv, Sk, D), dtype=torch.int8, device=dev)
+    ks = torch.empty((B, Hkv, (Sk + 15) // 16), dtype=torch.float32, device=dev)
+    vt = torch.empty((B, Hkv, D, (Sk + 63) // 64 * 64), dtype=torch.float16, device=dev)
+    mean = torch.empty((B, Hkv, D), dtype=key.dtype, device=dev) if return_mean else None
+    lib = _capi.load()
+    ws_bytes = lib.sage_k_mean_workspace_bytes(B, Hkv, Sk, D)
+    ws = torch.empty((max(ws_bytes, 4) + 3) // 4, dtype=torch.float32, device=dev)
+    with _on_device(dev):
+        _capi.call("sage_prep_kv_i8_smooth", key.data_ptr(), value.data_ptr(),
+                   mean.data_ptr() if mean is not None else _NULL, ws.data_ptr(), k8.data_ptr(), ks.data_ptr(),
+                   vt.data_ptr(), _dtype_code(key), B, Hkv, Sk, D, *kst, *vst, _stream(key))
+    return [k8, ks, vt, mean] if return_mean else [k8, ks, vt]
+
+
 def v_transpose(value: torch.Tensor, value_t: torch.Tensor, tensor_layout: int) -> torch.Tensor:
     """V -> fp16 V_T [B,H,D,ceil64(N)] written into ``value_t`` (reference
     v_transpose, csrc/attn_gfx11.cu:1889-1935)."""

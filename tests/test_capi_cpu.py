@@ -46,8 +46,9 @@ def test_size_helpers(lib):
     assert lib.sage_v_layout_padded_len(1) == 64
     assert lib.sage_v_layout_padded_len(64) == 64
     assert lib.sage_v_layout_padded_len(32891) == 32896
-    assert lib.sage_k_mean_workspace_bytes(2, 32, 8192, 128) == 2 * 32 * 32 * 128 * 4
-    assert lib.sage_k_mean_workspace_bytes(1, 40, 32891, 128) == 40 * 129 * 128 * 4
+    # one fp32 partial row per 1024-key chunk
+    assert lib.sage_k_mean_workspace_bytes(2, 32, 8192, 128) == 2 * 32 * 8 * 128 * 4
+    assert lib.sage_k_mean_workspace_bytes(1, 40, 32891, 128) == 40 * 33 * 128 * 4
     assert lib.sage_k_mean_workspace_bytes(0, 1, 1, 64) == 0
 
 
@@ -362,6 +363,39 @@ def test_prep_kv_zero_work_is_ok(lib):
     assert prep(lib, B=0, k=NULL) == _capi.OK
 
 
+def prep_smooth(lib, **kw):
+    a = dict(k=FAKE, v=FAKE, mean=NULL, ws=FAKE, k8=FAKE, ks=FAKE, vt=FAKE, dtype=1, B=1, H=2, S=100, D=128,
+             ksb=2 * 100 * 128, ksh=100 * 128, ksn=128, vsb=2 * 100 * 128, vsh=100 * 128, vsn=128, stream=NULL)
+    a.update(kw)
+    return lib.sage_prep_kv_i8_smooth(*a.values())
+
+
+@pytest.mark.parametrize(
+    "kw,code,msg",
+    [
+        (dict(dtype=2), _capi.ERR_INVALID_ARG, "dtype"),
+        (dict(D=96), _capi.ERR_UNSUPPORTED, "head_dim"),
+        (dict(B=-1), _capi.ERR_INVALID_ARG, "negative or zero"),
+        (dict(ws=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(k8=NULL), _capi.ERR_INVALID_ARG, "null"),
+        (dict(v=ODD), _capi.ERR_ALIGNMENT, "value"),
+        (dict(ksh=100 * 128 + 4), _capi.ERR_ALIGNMENT, "key"),
+        (dict(ws=ctypes.c_void_p(0x10002)), _capi.ERR_ALIGNMENT, "workspace"),
+        (dict(mean=ODD), _capi.ERR_ALIGNMENT, "key_mean"),
+        (dict(k8=ctypes.c_void_p(0x10004)), _capi.ERR_ALIGNMENT, "k_i8"),
+        (dict(S=1 << 31), _capi.ERR_UNSUPPORTED, "grid limits"),
+    ],
+)
+def test_prep_kv_smooth_validation(lib, kw, code, msg):
+    assert prep_smooth(lib, **kw) == code
+    assert msg in lib.sage_last_error().decode()
+
+
+def test_prep_kv_smooth_zero_work_is_ok(lib):
+    assert prep_smooth(lib, S=0) == _capi.OK
+    assert prep_smooth(lib, B=0, k=NULL, ws=NULL) == _capi.OK
+
+
 def test_split_workspace_bytes(lib):
     ws = lib.sage_attn_workspace_bytes
     # forced counts: items (B*Hq*ceil(Sq/256)) x splits x 256 rows x (D + 1) fp32; D = 64 non-causal
@@ -413,6 +447,20 @@ def test_automatic_plans_for_256_cus(lib):
     assert plan(True, 2, 144, 256, 4096, 128, False, 0) == (256, 8)
     # a workspace-size query agrees with the plan: (q-blocks - whole) * splits * 256 rows * (D + 1) fp32
     assert lib.sage_attn_workspace_bytes(1, 1, 3, 24576, 24576, 128, 0, 0) == 32 * 8 * 256 * 129 * 4
+
+
+def test_noalloc_refuses_splits_beyond_the_scratch(lib):
+    """sage_attn_i8_fwd_qfused_noalloc: a forced split count whose partials exceed the library's 64 MiB
+    scratch is refused before any launch (the pointers are never dereferenced)."""
+    need = lib.sage_attn_workspace_bytes(1, 1, 64, 4096, 4096, 128, 0, 16)
+    assert need > 64 << 20
+    rc = lib.sage_attn_i8_fwd_qfused_noalloc(FAKE, FAKE, FAKE, FAKE, NULL, FAKE, 1, 1, 64, 64, 4096, 4096, 128,
+                                             64 * 4096 * 128, 4096 * 128, 128, 64 * 4096 * 128, 4096 * 128, 128,
+                                             0, 0.088, 16, NULL)
+    assert rc == _capi.ERR_UNSUPPORTED
+    assert "scratch" in lib.sage_last_error().decode()
+    # a count that fits passes this check (and would launch): not called here
+    assert lib.sage_attn_workspace_bytes(1, 1, 4, 3000, 3000, 128, 0, 3) <= 64 << 20
 
 
 def test_v_layout_and_mean_validation(lib):

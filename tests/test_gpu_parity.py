@@ -248,6 +248,44 @@ def test_prep_kv_equals_quant_and_v_layout(cfg):
         assert torch.equal(k8, pro["k8"]) and torch.equal(vt, pro["v_t"])
 
 
+SMOOTH_PREP = [c for c in SMALL if c.dtype != "fp32" and c.smooth_k] + [
+    Config("smooth_d64_nhd_5000", 1, 3, 3, 5000, 64, "fp16", "NHD", False, True, k_offset_std=2.0),
+    Config("smooth_d128_fp16_8225", 2, 2, 1, 8225, 128, "fp16", "HND", True, True, k_offset_std=2.0),
+    Config("smooth_d128_bf16_17", 1, 2, 2, 17, 128, "bf16", "HND", False, True),
+    BASELINE_CONFIGS[2], BASELINE_CONFIGS[4]]
+
+
+@pytest.mark.parametrize("cfg", SMOOTH_PREP, ids=lambda c: c.name)
+def test_prep_kv_smooth_matches_oracle(cfg):
+    """K mean + K quantisation + V layout in two launches (the smooth_k prologue sageattn runs): the K
+    blocks finish the mean from the chunk sums themselves.  The mean, k_int8, k_scale and V_T equal
+    the oracle's bit for bit (C3 and C5 at full size, ragged lengths whose last K block of a head is
+    partial, NHD, GQA, both head dims and dtypes), and equal the three-launch path (mean_seq, then
+    prep_kv_int8 with that mean)."""
+    from sageattention import ops
+
+    _say(f"[prep_kv smooth] {cfg}")
+    lay = ops.HND if cfg.layout == "HND" else ops.NHD
+    _, k, v = make_inputs(cfg, seed=12)
+    kd, vd = k.cuda(), v.cuda()
+    k8, ks, vt, mean = ops.prep_kv_int8_smooth(kd, vd, lay, return_mean=True)
+    mean_ref = ops.mean_seq(kd, lay)
+    k8_ref, ks_ref, vt_ref = ops.prep_kv_int8(kd, vd, mean_ref, lay)
+    torch.cuda.synchronize()
+    assert torch.equal(mean, mean_ref)
+    assert torch.equal(k8, k8_ref) and torch.equal(ks, ks_ref) and torch.equal(vt, vt_ref)
+    kn, vn = to_np(k), to_np(v)
+    m_or = orc.k_mean(kn, cfg.dtype, cfg.layout)
+    assert np.array_equal(to_np(mean).view(np.uint16), m_or.view(np.uint16)), "K mean differs from the oracle"
+    k8_or, ks_or = orc.quant_per_block(orc.to_f32(orc.to_hnd(kn, cfg.layout), cfg.dtype), orc.K_GROUP, None,
+                                       orc.to_f32(m_or, cfg.dtype))
+    assert np.array_equal(to_np(k8), k8_or), "k_int8 differs from the oracle"
+    assert np.array_equal(to_np(ks).view(np.uint32), ks_or.view(np.uint32)), "k_scale differs from the oracle"
+    del k8_or
+    vt_or = orc.v_layout(vn, cfg.dtype, cfg.layout)
+    assert np.array_equal(to_np(vt).view(np.uint16), vt_or.view(np.uint16)), "V_T differs from the oracle"
+
+
 def test_qfused_large_scales_and_negative_scale():
     """The fused quantiser on the extreme-scale inputs (exact-softmax fallback) and with a negative
     sm_scale (negated q_int8, positive scales), against the two-kernel path."""
@@ -272,6 +310,35 @@ def test_qfused_large_scales_and_negative_scale():
     ops.qk_int8_sv_bf16_attn_qfused_t(qd, k8, vt, o2, ks, ops.HND, 1, -0.07, num_splits=1)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+def test_qfused_large_scales_on_causal_diagonal_tiles():
+    """Causal launches with few q-blocks run 128-row blocks, whose diagonal tiles the Q-fused kernel
+    takes through the pipelined step.  Its conversion-free softmax is exact only for q_scale * k_scale
+    below 0.49, and the block's scale scan covers the unmasked tiles only, so each diagonal tile's own
+    scales must pass that bar.  Outliers of 600 in one channel give q_scale * k_scale ~ 2.8 on two
+    diagonal tiles in a row of one wave (the first one moves the reference max, so the second does
+    not redo): in q-block 0 (keys 10-20 and 70-80, rows 96-127, whose unmasked range is empty) and in
+    q-block 5 of another head (keys 650-660 and 705-715, rows 704-735, whose unmasked tiles have
+    ordinary scales).  Every row is held to the oracle bar and the fused output to the two-kernel
+    path bit for bit."""
+    cfg = Config("large_scales_diag", 1, 4, 2, 1000, 128, "fp16", "HND", True, False)
+    _say(f"[large scales, diagonal tiles] {cfg}")
+    q, k, v = (t.float() for t in make_inputs(cfg, seed=13))
+    k[0, 0, 10:20, 7] = 600.0
+    k[0, 0, 70:80, 7] = 600.0
+    q[0, 0, 96:128, 7] = 600.0
+    k[0, 1, 650:660, 7] = 600.0
+    k[0, 1, 705:715, 7] = 600.0
+    q[0, 2, 704:736, 7] = 600.0
+    q, k, v = (t.to(torch.float16) for t in (q, k, v))
+    pro = gpu_prologue(cfg, q, k, v)
+    assert float(pro["q_scale"].max()) * float(pro["k_scale"].max()) > 4.0 / 3.0
+    o = gpu_attn(cfg, pro, q.dtype)
+    worst = check_rows_vs_oracle(cfg, pro, o, range(cfg.Hq), np.arange(cfg.q_len), cfg.dtype)
+    o_f, _, _, _ = gpu_fused(cfg, q, k, v)
+    assert torch.equal(o_f, o), f"max diff {(o_f.float() - o.float()).abs().max().item()}"
+    _say(f"  worst |gpu-oracle| = {worst:.3g}")
 
 
 # ------------------------------------------------------------------ BASELINE sizes
