@@ -444,6 +444,10 @@ def test_automatic_plans_for_256_cus(lib):
     assert plan(True, 1, 3, 24576, 24576, 128, False, 0) == (256, 8)     # 288 = 256 + 32
     assert plan(False, 1, 10, 2048, 2048, 128, False, 0) == (0, 3)       # 80 q-blocks
     assert plan(True, 1, 10, 4096, 4096, 64, False, 0) == (256, 4)       # 320 128-row q-blocks = 256 + 64
+    # 128-row q-blocks that fit one dispatch at two blocks per CU: a tail of up to half a round is split,
+    # a longer one runs whole beside the others
+    assert plan(True, 1, 12, 4096, 4096, 64, False, 0) == (256, 2)       # 384 = 256 + 128
+    assert plan(True, 1, 5, 11264, 11264, 64, False, 0) == (440, 1)      # 440 = 256 + 184
     assert plan(True, 2, 144, 256, 4096, 128, False, 0) == (256, 8)
     # a workspace-size query agrees with the plan: (q-blocks - whole) * splits * 256 rows * (D + 1) fp32
     assert lib.sage_attn_workspace_bytes(1, 1, 3, 24576, 24576, 128, 0, 0) == 32 * 8 * 256 * 129 * 4
