@@ -1,9 +1,9 @@
 """The product path itself -- ``sageattn`` and the fused-Q launch it makes -- at the BASELINE sizes, every
 output element written (NaN canaries), and the reference's own benchmark shapes in its NHD layout.
 
-* ``test_sageattn_full_size``: ``sageattn`` at NS, C3, C4 and C5 (what ``bench.py`` times: K mean when
-  smooth_k, K quantisation + V layout in one launch, the attention kernel that quantises Q itself, on the
-  persistent grid).  Its prologue inputs are checked bit-exact against the oracle, its output against the
+* ``test_sageattn_full_size``: ``sageattn`` at NS, C3, C4 and C5 (what ``bench.py`` times: K quantisation +
+  V layout in one launch -- with smooth_k, after the K mean's chunk-sum launch, the quantisation blocks
+  finishing the mean -- then the attention kernel that quantises Q itself, on the persistent grid).  Its prologue inputs are checked bit-exact against the oracle, its output against the
   oracle's rows (ends, tile and group boundaries, C5's ragged tail; the bars of test_gpu_parity), and against
   the two-kernel ops path (quant_qk_int8 + qk_int8_sv_bf16_attn_t, reference core.py:165-198) bit for
   bit whenever the launch runs unsplit (``SAGEATTN_KV_SPLITS=1`` forces that for a split plan).
