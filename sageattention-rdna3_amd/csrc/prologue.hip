@@ -5,7 +5,7 @@
 //   * K quantisation + V layout in one launch, and for smooth_k the K mean's
 //     chunk sums followed by one launch that finishes the mean inside its K
 //     quantisation blocks (what sageattn runs before the attention kernel).
-// All three are HBM-bound byte shuffles: one 16-byte load per lane per row
+// All are HBM-bound byte shuffles: one 16-byte load per lane per row
 // piece, wave64 reductions, 8/16-byte coalesced stores, no MFMA.
 //
 // Bit-exactness: the quantiser's arithmetic follows the reference order
@@ -60,7 +60,7 @@ struct QuantUnit {
   static constexpr int CPR = D / 8;       // 16-byte chunks per row
   static constexpr int RPI = 32 / CPR;    // rows per iteration per half wave
   static constexpr int ITER = 16 / RPI;   // iterations per lane
-  const QuantParams* pp;  // a pointer, so that units can be assigned
+  const QuantParams* pp;  // the launch's parameters
   bool valid, is_q;
   int64_t bh;
   int ub, S, half, li, cc, row0;
