@@ -5,7 +5,10 @@ Workload (BASELINE.json metric): ``sageattn`` at B=1, H=32, S=16384, D=128,
 bf16, HND, causal, smooth_k=False.  A step is one full ``sageattn`` call (V
 layout + INT8 quant of K + fused attention that quantises Q itself and runs
 INT8-QK^T / fp16-PV) on inputs already resident in HBM; ``value`` is effective
-TOPS of the whole step: 4*B*H*D*S(S+1)/2 / step time.
+TOPS of the whole step: 4*B*H*D*S(S+1)/2 / step time.  Order: the inputs are
+generated on the CPU and copied over, the per-kernel probes of the same
+tensors run (each settled first: the GPU clock ramps up over its first ~50 ms
+of work after an idle period), then W warmup steps and the K timed steps.
 
 ``roofline`` is that attention kernel alone, timed with HIP events on the
 stream it is launched on (torch's current stream): achieved = the same ops /
@@ -180,16 +183,38 @@ def queue_ahead(dev):
 _BUSY = {}
 
 
+SETTLE_MS = 60.0
+
+
+def settle(fn, ms=SETTLE_MS):
+    """Call fn (at least 3 times) until the GPU has run it for ``ms`` milliseconds of wall time, and return the
+    number of calls.  After an idle period (the CPU input generation) the GPU's clock ramps up over its first
+    ~50 ms of work: NS steps measured 1.83 ms averaged over the first 10 after a 2 s idle, 1.64 ms over the
+    next 10 and 1.607 ms from the 30th on (C3: 1.10, 0.98, then 0.915), so a probe timed straight after an
+    idle period reads the ramp, not the kernel."""
+    import torch
+
+    t0 = time.perf_counter()
+    calls, batch = 0, 1
+    while True:
+        for _ in range(batch):
+            fn()
+        torch.cuda.synchronize()
+        calls += batch
+        if calls >= 3 and (time.perf_counter() - t0) * 1e3 >= ms:
+            return calls
+        batch = min(2 * batch, 256)
+
+
 def timed_launches(fn, n, stream, dev, queue=True):
-    """Average time of one call of fn over n back-to-back calls, with HIP events on the launch stream (3 warm
-    calls first; with queue, the GPU kept busy while the n calls are enqueued -- for kernels shorter than the
-    host's per-call time)."""
+    """Average time of one call of fn over n back-to-back calls, with HIP events on the launch stream (settled
+    first; with queue, the GPU kept busy while the n calls are enqueued -- for kernels shorter than the host's
+    per-call time)."""
     import torch
 
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    for _ in range(3):
-        fn()
+    settle(fn)
     if queue:
         torch.cuda.synchronize(dev)
         queue_ahead(dev)
@@ -234,9 +259,7 @@ def step_breakdown(cfg, q, k, v, n, stream, queue=False):
             ev[2].record(stream)
         return o
 
-    for _ in range(3):
-        one(None)
-    torch.cuda.synchronize()
+    settle(lambda: one(None))
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
     if queue:
         queue_ahead(q.device)
@@ -353,8 +376,7 @@ def direct_probe(dev, n):
     def timed(fn):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        for _ in range(3):
-            fn()
+        settle(fn)
         e0.record(stream)
         for _ in range(n):
             fn()
@@ -473,9 +495,7 @@ def reference_shapes_probe(dev, n, names=None, modes=("auto", "1")):
                         os.environ.pop("SAGEATTN_KV_SPLITS", None)
                     else:
                         os.environ["SAGEATTN_KV_SPLITS"] = mode
-                    for _ in range(3):
-                        sageattn(q, k, v, tensor_layout="NHD", is_causal=False)
-                    torch.cuda.synchronize()
+                    settle(lambda: sageattn(q, k, v, tensor_layout="NHD", is_causal=False), SETTLE_MS / 3)
                     e0 = torch.cuda.Event(enable_timing=True)
                     e1 = torch.cuda.Event(enable_timing=True)
                     e0.record()
@@ -670,37 +690,11 @@ def main():
         kernels_only(cfg, q, k, v, args.steps)
         return
 
-    def step():
-        return sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth)
-
-    for i in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done")
-
-    sampler = SclkSampler(dev)
-    with sampler:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    ms_step = (t1 - t0) * 1e3 / args.steps
-    ops_step = attn_ops(B, Hq, S, S, D, causal)
-    value = ops_step / (ms_step * 1e-3) / 1e12
-    log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS; shader clock during the "
-        f"steps (sysfs) {sampler.mhz()} MHz ({sampler.kind or 'not readable'}, {len(sampler.samples)} samples)")
-
-    # ---- the same steps' launches with HIP events between them (in-step kernel times)
     lay = ops.HND if layout == "HND" else ops.NHD
     stream = torch.cuda.current_stream(dev)
-    bd = step_breakdown(cfg, q, k, v, args.steps, stream, queue=ms_step < 0.25)
-    bd["ms_per_step"] = round(ms_step, 5)
-    bd["unaccounted_us"] = round((ms_step - bd["sum_ms"]) * 1e3, 2)
-    log(f"[bench] in-step: prologue {bd['prologue_us']} us + attention {bd['attention_ms']:.4f} ms + gap "
-        f"{bd['gap_between_steps_us']} us = {bd['sum_ms']:.4f} ms of GPU time; sageattn steps {ms_step:.4f} ms")
-
-    # ---- per-kernel timing with HIP events on the launch stream, back to back
+    # ---- per-kernel timing with HIP events on the launch stream, back to back.  These probes run before
+    # the headline steps: after the idle of the CPU input generation the GPU clock ramps up over its first
+    # ~50 ms of work, which a short warm-up (the driver's W) does not cover; each probe settles first.
     mean = ops.mean_seq(k, lay) if smooth else torch.empty(0, device=dev, dtype=q.dtype)
     q8, qs, k8, ks = ops.quant_qk_int8(q, k, mean, lay, D ** -0.5)
     vt = torch.empty(B, Hkv, D, (S + 63) // 64 * 64, device=dev, dtype=torch.float16)
@@ -711,10 +705,6 @@ def main():
         return timed_launches(fn, n, stream, dev, queue)
 
     n_k = max(args.steps, 10)
-    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n_k,
-                    queue=False)
-    ms_attn_unfused = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5),
-                            n_k, queue=False)
     # The prologue kernels stream HBM: back to back on the same tensors, part of their traffic would hit the
     # L2 / Infinity Cache (256 MB), so each launch gets its own input set out of NROT (together well past the
     # caches), and the output of a set is written while the next set is read.
@@ -744,7 +734,41 @@ def main():
     ms_prep_smooth = (timed(rotated(lambda i: qouts.__setitem__(i, ops.prep_kv_int8_smooth(kr[i], vr[i], lay))), n_k)
                       if smooth else None)
     del qr, kr, vr, vtr, qouts
+    # the attention kernel alone, last, so that the headline steps follow the same MFMA-bound work
+    ms_attn_unfused = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5),
+                            n_k, queue=False)
+    ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n_k,
+                    queue=False)
     torch.cuda.synchronize()
+
+    def step():
+        return sageattn(q, k, v, tensor_layout=layout, is_causal=causal, smooth_k=smooth)
+
+    for i in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done")
+
+    sampler = SclkSampler(dev)
+    with sampler:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    ops_step = attn_ops(B, Hq, S, S, D, causal)
+    value = ops_step / (ms_step * 1e-3) / 1e12
+    log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS; shader clock during the "
+        f"steps (sysfs) {sampler.mhz()} MHz ({sampler.kind or 'not readable'}, {len(sampler.samples)} samples)")
+
+    # ---- the same steps' launches with HIP events between them (in-step kernel times)
+    bd = step_breakdown(cfg, q, k, v, args.steps, stream, queue=ms_step < 0.25)
+    bd["ms_per_step"] = round(ms_step, 5)
+    bd["unaccounted_us"] = round((ms_step - bd["sum_ms"]) * 1e3, 2)
+    log(f"[bench] in-step: prologue {bd['prologue_us']} us + attention {bd['attention_ms']:.4f} ms + gap "
+        f"{bd['gap_between_steps_us']} us = {bd['sum_ms']:.4f} ms of GPU time; sageattn steps {ms_step:.4f} ms")
+
     # the roofline's kernel time: the attention kernel inside the steps (what ms_per_step contains)
     achieved = ops_step / (bd["attention_ms"] * 1e-3) / 1e12
     achieved_b2b = ops_step / (ms_attn * 1e-3) / 1e12
@@ -795,6 +819,10 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "before_warmup": "the per-kernel probes of the same tensors (prologue kernels, then the attention kernel, "
+                         f"each run for {SETTLE_MS:.0f} ms before its timed launches): the W warmup steps follow "
+                         "GPU work, not the idle of the CPU input generation, after which the clock ramps up over "
+                         "~50 ms of work",
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
