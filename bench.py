@@ -186,7 +186,7 @@ _BUSY = {}
 SETTLE_MS = 60.0
 
 
-def settle(fn, ms=SETTLE_MS):
+def settle(fn, ms=SETTLE_MS, label=None):
     """Call fn (at least 3 times) until the GPU has run it for ``ms`` milliseconds of wall time, and return the
     number of calls.  After an idle period (the CPU input generation) the GPU's clock ramps up over its first
     ~50 ms of work: NS steps measured 1.83 ms averaged over the first 10 after a 2 s idle, 1.64 ms over the
@@ -202,11 +202,13 @@ def settle(fn, ms=SETTLE_MS):
         torch.cuda.synchronize()
         calls += batch
         if calls >= 3 and (time.perf_counter() - t0) * 1e3 >= ms:
+            if label:
+                log(f"[bench] {label}: settled over {calls} calls")
             return calls
         batch = min(2 * batch, 256)
 
 
-def timed_launches(fn, n, stream, dev, queue=True):
+def timed_launches(fn, n, stream, dev, queue=True, label=None):
     """Average time of one call of fn over n back-to-back calls, with HIP events on the launch stream (settled
     first; with queue, the GPU kept busy while the n calls are enqueued -- for kernels shorter than the host's
     per-call time)."""
@@ -214,7 +216,7 @@ def timed_launches(fn, n, stream, dev, queue=True):
 
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    settle(fn)
+    settle(fn, label=label)
     if queue:
         torch.cuda.synchronize(dev)
         queue_ahead(dev)
@@ -226,7 +228,7 @@ def timed_launches(fn, n, stream, dev, queue=True):
     return e0.elapsed_time(e1) / n
 
 
-def step_breakdown(cfg, q, k, v, n, stream, queue=False):
+def step_breakdown(cfg, q, k, v, n, stream, queue=False, label=None):
     """The launches of one ``sageattn`` INT8 step -- the K prologue (smooth_k: the K mean's chunk sums, then K
     quantisation finishing the mean + V layout; else K quantisation + V layout in one launch), then the
     attention kernel that quantises Q (and the key-split merge when its plan splits) -- issued through the ops
@@ -259,7 +261,7 @@ def step_breakdown(cfg, q, k, v, n, stream, queue=False):
             ev[2].record(stream)
         return o
 
-    settle(lambda: one(None))
+    settle(lambda: one(None), label=label)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n)]
     if queue:
         queue_ahead(q.device)
@@ -701,8 +703,8 @@ def main():
     ops.v_transpose(v, vt, lay)
     o = torch.empty_like(q)
 
-    def timed(fn, n, queue=True):
-        return timed_launches(fn, n, stream, dev, queue)
+    def timed(fn, n, queue=True, label=None):
+        return timed_launches(fn, n, stream, dev, queue, label)
 
     n_k = max(args.steps, 10)
     # The prologue kernels stream HBM: back to back on the same tensors, part of their traffic would hit the
@@ -738,7 +740,7 @@ def main():
     ms_attn_unfused = timed(lambda: ops.qk_int8_sv_bf16_attn_t(q8, k8, vt, o, qs, ks, lay, int(causal), D ** -0.5),
                             n_k, queue=False)
     ms_attn = timed(lambda: ops.qk_int8_sv_bf16_attn_qfused_t(q, k8, vt, o, ks, lay, int(causal), D ** -0.5), n_k,
-                    queue=False)
+                    queue=False, label="attention back-to-back loop")
     torch.cuda.synchronize()
 
     def step():
@@ -749,21 +751,28 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done")
 
-    sampler = SclkSampler(dev)
-    with sampler:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
     ops_step = attn_ops(B, Hq, S, S, D, causal)
     value = ops_step / (ms_step * 1e-3) / 1e12
-    log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS; shader clock during the "
-        f"steps (sysfs) {sampler.mhz()} MHz ({sampler.kind or 'not readable'}, {len(sampler.samples)} samples)")
+    # the shader clock as sysfs reports it, over as many untimed steps right after: each read queries the SMU,
+    # so no read runs beside the timed steps (kernel traces: the attention calls of steps timed beside the
+    # sampler ran 1.7% slower than those of the in-step loop that followed, twice; without it 1.0%, once)
+    sampler = SclkSampler(dev)
+    with sampler:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    log(f"[bench] {args.steps} steps: {ms_step:.4f} ms/step, {value:.1f} effective TOPS; shader clock over as many "
+        f"untimed steps after them (sysfs) {sampler.mhz()} MHz ({sampler.kind or 'not readable'}, "
+        f"{len(sampler.samples)} samples)")
 
     # ---- the same steps' launches with HIP events between them (in-step kernel times)
-    bd = step_breakdown(cfg, q, k, v, args.steps, stream, queue=ms_step < 0.25)
+    bd = step_breakdown(cfg, q, k, v, args.steps, stream, queue=ms_step < 0.25, label="in-step loop")
     bd["ms_per_step"] = round(ms_step, 5)
     bd["unaccounted_us"] = round((ms_step - bd["sum_ms"]) * 1e3, 2)
     log(f"[bench] in-step: prologue {bd['prologue_us']} us + attention {bd['attention_ms']:.4f} ms + gap "
@@ -874,7 +883,7 @@ def main():
         "configs": configs,
         "reference_shapes": ref_shapes,
         "device": {"name": props.name, "cus": props.multi_processor_count,
-                   "sclk_mhz_sysfs_during_steps": sampler.mhz(), "sclk_source": sampler.kind,
+                   "sclk_mhz_sysfs_untimed_steps": sampler.mhz(), "sclk_source": sampler.kind,
                    "peak_clock_assumed_mhz": 2400},
         "cpu_baseline": cpu,
     }
