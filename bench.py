@@ -355,6 +355,76 @@ def kernels_only(cfg, q, k, v, n):
     log(f"[bench] kernels-only: {n} x path kernels + {n} x 1 GiB copy done")
 
 
+def under_profiler():
+    """True when this process itself runs under rocprofv3 (its tool library is preloaded)."""
+    return "rocprofiler" in os.environ.get("LD_PRELOAD", "") or any(k.startswith("ROCPROF") for k in os.environ)
+
+
+def _counter_means(csv_path, counter):
+    """{short kernel name: mean over dispatches of the counter (summed over its dimensions)} of a rocprofv3
+    counter_collection.csv; the 1 GiB device copy is named "copy_1GiB"."""
+    import csv
+    import collections
+
+    per = collections.defaultdict(float)
+    names = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            if r.get("Counter_Name") != counter:
+                continue
+            name = r["Kernel_Name"]
+            if "sage::" in name and "(anonymous namespace)::" in name:
+                short = name.split("(anonymous namespace)::")[1].split("(sage")[0]
+            elif "copyBuffer" in name:
+                short = "copy_1GiB"
+            else:
+                continue
+            per[r["Dispatch_Id"]] += float(r["Counter_Value"])
+            names[r["Dispatch_Id"]] = short
+    acc = collections.defaultdict(list)
+    for d, v in per.items():
+        acc[names[d]].append(v)
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def measure_traffic(config, D, steps=3):
+    """HBM bytes per launch of the fused-Q attention kernel, measured now: two rocprofv3 --pmc runs (FETCH_SIZE,
+    then WRITE_SIZE, one counter each) of this script's --kernels-only mode for the same config, each in a child
+    process while this one waits, each counter's KiB per dispatch scaled by what it reads for the 1 GiB device
+    copy that mode ends with (FETCH_SIZE reads the copy as 0.5 GiB, WRITE_SIZE as 1 GiB).  None when rocprofv3
+    is not installed or a run gives no figure."""
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    res = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="sage_pmc_", dir="/tmp")
+        cmd = ["timeout", "-s", "KILL", "150", exe, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "p",
+               "--", sys.executable, os.path.abspath(__file__), "--config", config, "--kernels-only",
+               "--steps", str(steps)]
+        log(f"[bench] traffic: rocprofv3 --pmc {counter} of bench.py --config {config} --kernels-only ...")
+        env = dict(os.environ, TMPDIR="/tmp")
+        with open(os.path.join(d, "run.log"), "w") as out:
+            rc = subprocess.run(cmd, cwd="/tmp", env=env, stdout=out, stderr=subprocess.STDOUT).returncode
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        means = _counter_means(files[0], counter) if files else {}
+        attn = [v for k, v in means.items() if k.replace(" ", "").startswith(f"attn_fwd_kernel<{D},3,")]
+        # rocprofv3 can end with a fault of its own after the program and its results are complete (rc 139);
+        # the figure is used whenever the results hold both kernels
+        if not attn or not means.get("copy_1GiB"):
+            log(f"[bench] traffic: no {counter} figure (rc {rc}; log in {d})")
+            return None
+        res[counter] = attn[0] * 1024.0 * ((1 << 30) / (means["copy_1GiB"] * 1024.0))
+        shutil.rmtree(d, ignore_errors=True)
+    return {"fetch_bytes": res["FETCH_SIZE"], "write_bytes": res["WRITE_SIZE"],
+            "bytes": res["FETCH_SIZE"] + res["WRITE_SIZE"]}
+
+
 # direct (unquantised) kernel: the largest D=128 self-attention shape the reference's dispatch sends to it
 DIRECT_CFG = (1, 32, 32, 2048, 128, "bf16", "HND", True, False)
 
@@ -639,6 +709,9 @@ def main():
     ap.add_argument("--config", default="NS", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU oracle work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="take roofline.traffic from the committed profile instead of two rocprofv3 --pmc child runs "
+                         "(also skipped with --no-probes and when this process runs under rocprofv3)")
     ap.add_argument("--no-probes", action="store_true",
                     help="skip the direct-kernel, reference-shape and per-config probes (kernel traces of the NS "
                          "workload alone)")
@@ -803,17 +876,31 @@ def main():
         configs = {name: config_probe(name, dev, n_k) for name in args.configs.split(",") if name}
     ref_shapes = None if args.no_probes or "reference" in skip else reference_shapes_probe(dev, n_k)
 
-    # HBM bytes per attention launch: not measured in this run (counters need their own rocprofv3 --pmc
-    # runs); the figure of the committed profile of this workload, labelled as such
+    # HBM bytes per attention launch, measured now by two rocprofv3 --pmc child runs (counters need runs of their
+    # own); else the committed profile's figure of this workload, labelled as such
+    alg_bytes = (2 * nq + nk + 2 * B * Hkv * D * ((S + 63) // 64 * 64) + 2 * nq
+                 + 4 * B * Hkv * ((S + 15) // 16))  # bf16 Q, int8 K, fp16 V_T and k scales read, O written
+    meas = None
+    if not (args.no_traffic or args.no_probes or under_profiler()):
+        meas = measure_traffic(args.config, D)
     traffic = None
     traffic_source = None
-    tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")
-    if os.path.exists(tfile):
-        with open(tfile) as f:
-            traffic = json.load(f).get("attn_bytes_per_launch")
-        traffic_source = (f"profiles/hbm_traffic_{args.config}.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of "
-                          f"bench.py --kernels-only, each scaled by the same counter on a 1 GiB device copy "
-                          f"(committed profile, not measured in this run)")
+    traffic_parts = None
+    if meas is not None:
+        traffic = round(meas["bytes"])
+        traffic_parts = {"fetch_bytes": round(meas["fetch_bytes"]), "write_bytes": round(meas["write_bytes"])}
+        traffic_source = ("measured in this run: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one run each) of bench.py "
+                          "--kernels-only in a child process, each scaled by the same counter on a 1 GiB device copy")
+        log(f"[bench] traffic: {traffic / 1e6:.1f} MB per attention launch ({traffic / alg_bytes:.2f}x the "
+            f"{alg_bytes / 1e6:.1f} MB it must move)")
+    else:
+        tfile = os.path.join(REPO, "profiles", f"hbm_traffic_{args.config}.json")
+        if os.path.exists(tfile):
+            with open(tfile) as f:
+                traffic = json.load(f).get("attn_bytes_per_launch")
+            traffic_source = (f"profiles/hbm_traffic_{args.config}.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                              f"of bench.py --kernels-only, each scaled by the same counter on a 1 GiB device copy "
+                              f"(committed profile, not measured in this run)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -855,6 +942,9 @@ def main():
             "frac": round(achieved / PEAK_INT8_TOPS, 4),
             "traffic": traffic,
             "traffic_source": traffic_source,
+            "traffic_parts": traffic_parts,
+            "algorithmic_bytes": alg_bytes,
+            "traffic_over_algorithmic": round(traffic / alg_bytes, 3) if traffic else None,
             "kernel": "attn_fwd_kernel (int8 QK, Q quantised in the kernel)",
             "kernel_ms": bd["attention_ms"],
             "kernel_ms_source": "HIP events around the attention launch inside the steps (step_breakdown)",
