@@ -54,6 +54,7 @@
 //   * the epilogue stages each wave's output rows in LDS and writes whole
 //     rows; non-causal launches that leave CUs idle can split key ranges,
 //     merged by attn_merge_kernel with the partial LSEs.
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <type_traits>
@@ -131,17 +132,32 @@ constexpr bool kSmallShape = true;
 #include "attn_body.inc"
 }  // namespace w4
 
+// A lone 128-row block on a CU takes this fraction of a 256-row block's time
+// per key tile step (the D = 128 direct kernel on MI355X, B1 H32 S2048
+// causal: 0.97 against 1.38 us).
+constexpr double kLoneHalfBlockTile = 0.70;
+
 // The shape a launch runs: w4 for D = 64 non-causal launches, and for causal
 // launches whose 256-row q-blocks would fill at most half the CUs (their
 // 128-row q-blocks then fill twice as many, one block per CU; B1 H8 S4096
 // D128 INT8: -27%; the D = 128 direct kernel, whose 98 KB of LDS fits once per
 // CU, at B1 H8/H16 S1024-2048: -27% to -32%); w8 for the rest (a causal launch
-// of 256 q-blocks +4%, of 2048 +4% in w4; the D = 128 direct one of 256
-// q-blocks +9%).
-bool small_blocks(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len) {
+// of 256 q-blocks +4%, of 2048 +4% in w4).  The D = 128 direct kernel also
+// runs w4 when its 256-row q-blocks fill one round and the causal cost model
+// rates the 128-row q-blocks faster: with one block resident per CU they run
+// as a persistent grid in which the snake schedule gives each block a heavy
+// and a light q-block (B1 H32 S2048, B2 H16 S2048: -17%, B1 H24 S2048: -15%,
+// B1 H16 S4096: -21%; the model keeps B1 H32 S1536 in w8, where a block would
+// get two heavy q-blocks: +15% in w4).
+bool small_blocks(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len,
+                  bool direct) {
   if (is_causal == 0) return head_dim == 64;
   const int64_t qblocks = batch * q_heads * ((q_len + 255) / 256);
-  return qblocks > 0 && qblocks * 2 <= device_cus();
+  if (qblocks <= 0) return false;
+  if (qblocks * 2 <= device_cus()) return true;
+  if (!direct || head_dim != 128 || qblocks > device_cus()) return false;
+  return kLoneHalfBlockTile * w4::causal_blocks_cost<128, w4::kQkBf16>(batch * q_heads, q_len, kv_len) <
+         w8::causal_blocks_cost<128, w8::kQkBf16>(batch * q_heads, q_len, kv_len);
 }
 
 }  // namespace sage
@@ -187,16 +203,18 @@ void* scratch_address(const char* fn) {
 
 // attn_fwd of the block shape the launch runs (the arguments include head_dim and is_causal again)
 template <typename... Args>
-int run_attn(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len, int qk, Args... args) {
-  return small_blocks(head_dim, is_causal, batch, q_heads, q_len) ? w4::attn_fwd(qk, args...)
-                                                                   : w8::attn_fwd(qk, args...);
+int run_attn(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len, int qk,
+             Args... args) {
+  const bool direct = qk == w8::kQkF16 || qk == w8::kQkBf16 || qk == w8::kQkF16V;
+  return small_blocks(head_dim, is_causal, batch, q_heads, q_len, kv_len, direct) ? w4::attn_fwd(qk, args...)
+                                                                                  : w8::attn_fwd(qk, args...);
 }
 
 // The plan of the shape the launch runs and its workspace bytes (or a negative status).
 int64_t split_plan(bool quantized, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len, int64_t head_dim,
                    int is_causal, int num_splits, int64_t* whole, int* splits) {
   int64_t r;
-  if (small_blocks(head_dim, is_causal, batch, q_heads, q_len)) {
+  if (small_blocks(head_dim, is_causal, batch, q_heads, q_len, kv_len, !quantized)) {
     w4::SplitPlan sp;
     r = w4::attn_split_plan(quantized, batch, q_heads, q_len, kv_len, head_dim, is_causal, num_splits, &sp);
     *whole = sp.nfull;
@@ -218,7 +236,7 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
                                 int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                                 int is_causal, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale,
                   k_scale, out_dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim,
                   q_len * head_dim, head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0,
                   o_stride_b, o_stride_h, o_stride_n, is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd");
@@ -231,7 +249,7 @@ extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, cons
                                     int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                                     int is_causal, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8, q_i8, k_i8, value_t, out, lse, q_scale,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8, q_i8, k_i8, value_t, out, lse, q_scale,
                   k_scale, out_dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim,
                   q_len * head_dim, head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0,
                   o_stride_b, o_stride_h, o_stride_n, is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd_lse");
@@ -246,7 +264,7 @@ extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const vo
                                     int is_causal, double sm_scale, int num_splits, void* workspace,
                                     int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, dtype == SAGE_DTYPE_BF16 ? w8::kQkBf16 : w8::kQkF16,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, dtype == SAGE_DTYPE_BF16 ? w8::kQkBf16 : w8::kQkF16,
                   query, key, value_t, out, lse, nullptr, nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len,
                   head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b, k_stride_h, k_stride_n, 0, 0, 0,
                   o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes,
@@ -263,7 +281,7 @@ extern "C" int sage_attn_direct_fwd_vrows(const void* query, const void* key, co
                                           int is_causal, double sm_scale, int num_splits, void* workspace,
                                           int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkF16V, query, key, value, out, lse, nullptr,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkF16V, query, key, value, out, lse, nullptr,
                   nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
                   q_stride_n, k_stride_b, k_stride_h, k_stride_n, v_stride_b, v_stride_h, v_stride_n, o_stride_b,
                   o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream,
@@ -279,7 +297,7 @@ extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, co
                                        int is_causal, double sm_scale, int num_splits, void* workspace,
                                        int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
                   k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
                   q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b,
                   o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream,
@@ -296,7 +314,7 @@ extern "C" int sage_attn_i8_fwd_qfused_vrows(const void* query, const int8_t* k_
                                              int is_causal, double sm_scale, int num_splits, void* workspace,
                                              int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8FV, query, k_i8, value, out, lse, nullptr,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8FV, query, k_i8, value, out, lse, nullptr,
                   k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
                   q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, v_stride_b, v_stride_h,
                   v_stride_n, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace,
@@ -329,7 +347,7 @@ extern "C" int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* 
     ws = scratch_address(fn);
     if (ws == nullptr) return SAGE_ERR_HIP;
   }
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
                   k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
                   q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b,
                   o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, ws, ws != nullptr ? kScratchBytes : 0,

@@ -153,6 +153,43 @@ def test_direct_dispatch_range_sampled_rows(cfg):
     _say(f"  worst |gpu-oracle| = {worst:.3g}")
 
 
+@pytest.mark.parametrize("cfg", [
+    Config("paired_b1h32_s2048", 1, 32, 32, 2048, 128, "bf16", "HND", True, False),
+    Config("paired_b2h16_s2048_nhd_gqa", 2, 16, 4, 2048, 128, "fp16", "NHD", True, False),
+], ids=lambda c: c.name)
+def test_direct_causal_paired_schedule(cfg):
+    """Causal D = 128 direct launches whose 256-row q-blocks fill one round run 128-row q-blocks as a
+    persistent grid of one block per CU, each block a heavy and a light q-block in turn: every output
+    element and LSE written (NaN canaries), sampled rows of every head against the oracle, and the LSE
+    of those rows."""
+    from sageattention import _capi, ops
+
+    _say(f"[direct paired] {cfg}")
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert _capi.split_plan(False, cfg.B, cfg.Hq, cfg.S, cfg.S, cfg.D, True, 0) == (cfg.B * cfg.Hq * cfg.S // 128, 1)
+    q, k, v = make_inputs(cfg, seed=16)
+    lay = ops.HND if cfg.layout == "HND" else ops.NHD
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    vt = torch.empty(cfg.B, cfg.Hkv, cfg.D, cfg.S, device="cuda", dtype=torch.float16)
+    ops.v_transpose(vd, vt, lay)
+    o = torch.full(qd.shape, float("nan"), device="cuda", dtype=qd.dtype)
+    lse = torch.full((cfg.B, cfg.Hq, cfg.S), float("nan"), device="cuda", dtype=torch.float32)
+    fn = ops.bf16_attn_t if cfg.dtype == "bf16" else ops.fp16_attn_t
+    fn(qd, kd, vt, o, lay, 1, cfg.D ** -0.5, 0, lse=lse)
+    torch.cuda.synchronize()
+    assert not bool(torch.isnan(o).any()) and bool(torch.isfinite(lse).all())
+    rows = sample_rows(cfg.q_len, 24, np.random.default_rng(1))
+    worst = check_direct_rows(cfg, q, k, vt, o, range(cfg.Hq), rows, cfg.D ** -0.5)
+    q32 = orc.to_f32(orc.to_hnd(to_np(q), cfg.layout), cfg.dtype)
+    k32 = orc.to_f32(orc.to_hnd(to_np(k), cfg.layout), cfg.dtype)
+    got = to_np(lse).astype(np.float64)
+    for b in range(cfg.B):
+        for h in (0, cfg.Hq - 1):
+            ref = orc.attn_direct_lse_rows(q32, k32, cfg.D ** -0.5, b, h, rows, True)
+            assert np.all(np.abs(got[b, h, rows] - ref) <= 2e-4 + 2e-6 * np.abs(ref))
+    _say(f"  worst |gpu-oracle| = {worst:.3g}")
+
+
 @pytest.mark.parametrize("cfg", [DIRECT_SMALL[1], DIRECT_SMALL[2], DIRECT_SMALL[4], DIRECT_SMALL[9]],
                          ids=lambda c: c.name)
 def test_direct_lse_vs_oracle(cfg):
