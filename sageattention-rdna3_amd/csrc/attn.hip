@@ -133,30 +133,34 @@ constexpr bool kSmallShape = true;
 }  // namespace w4
 
 // A lone 128-row block on a CU takes this fraction of a 256-row block's time
-// per key tile step (the D = 128 direct kernel on MI355X, B1 H32 S2048
-// causal: 0.97 against 1.38 us).
-constexpr double kLoneHalfBlockTile = 0.70;
+// per key tile step (MI355X, B1 H32 S2048 causal: the D = 128 direct kernel
+// 0.97 against 1.38 us; fitted to the Q-fused INT8 kernel's paired launches at
+// B1 H16 S4096 and B1 H32 S2048: 0.77).
+constexpr double kLoneHalfBlockTileDirect = 0.70;
+constexpr double kLoneHalfBlockTileI8 = 0.77;
 
 // The shape a launch runs: w4 for D = 64 non-causal launches, and for causal
 // launches whose 256-row q-blocks would fill at most half the CUs (their
 // 128-row q-blocks then fill twice as many, one block per CU; B1 H8 S4096
 // D128 INT8: -27%; the D = 128 direct kernel, whose 98 KB of LDS fits once per
 // CU, at B1 H8/H16 S1024-2048: -27% to -32%); w8 for the rest (a causal launch
-// of 256 q-blocks +4%, of 2048 +4% in w4).  The D = 128 direct kernel also
-// runs w4 when its 256-row q-blocks fill one round and the causal cost model
-// rates the 128-row q-blocks faster: with one block resident per CU they run
-// as a persistent grid in which the snake schedule gives each block a heavy
-// and a light q-block (B1 H32 S2048, B2 H16 S2048: -17%, B1 H24 S2048: -15%,
-// B1 H16 S4096: -21%; the model keeps B1 H32 S1536 in w8, where a block would
-// get two heavy q-blocks: +15% in w4).
+// of 2048 +4% in w4).  A causal D = 128 launch also runs w4 when its 256-row
+// q-blocks fill one round and the causal cost model rates the 128-row q-blocks
+// faster: with one block resident per CU they run as a persistent grid in
+// which the snake schedule gives each block a heavy and a light q-block.
+// Direct kernel: B1 H32 S2048, B2 H16 S2048 -17%, B1 H24 S2048 -15%,
+// B1 H16 S4096 -21%; Q-fused INT8 kernel: B1 H16 S4096, B2 H8 S4096 -15%,
+// B1 H12 S4096 -19%, B1 H32 S2048 -10%.  The model keeps B1 H32 S1536 direct
+// in w8, where a block would get two heavy q-blocks (+15% in w4).
 bool small_blocks(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len,
                   bool direct) {
   if (is_causal == 0) return head_dim == 64;
   const int64_t qblocks = batch * q_heads * ((q_len + 255) / 256);
   if (qblocks <= 0) return false;
   if (qblocks * 2 <= device_cus()) return true;
-  if (!direct || head_dim != 128 || qblocks > device_cus()) return false;
-  return kLoneHalfBlockTile * w4::causal_blocks_cost<128, w4::kQkBf16>(batch * q_heads, q_len, kv_len) <
+  if (head_dim != 128 || qblocks > device_cus()) return false;
+  return (direct ? kLoneHalfBlockTileDirect : kLoneHalfBlockTileI8) *
+             w4::causal_blocks_cost<128, w4::kQkBf16>(batch * q_heads, q_len, kv_len) <
          w8::causal_blocks_cost<128, w8::kQkBf16>(batch * q_heads, q_len, kv_len);
 }
 

@@ -449,14 +449,18 @@ def test_automatic_plans_for_256_cus(lib):
     assert plan(True, 1, 12, 4096, 4096, 64, False, 0) == (256, 2)       # 384 = 256 + 128
     assert plan(True, 1, 5, 11264, 11264, 64, False, 0) == (440, 1)      # 440 = 256 + 184
     assert plan(True, 2, 144, 256, 4096, 128, False, 0) == (256, 8)
-    # causal D = 128 direct launches whose 256-row q-blocks fill one round: 128-row q-blocks on a persistent
-    # grid (one block per CU, a heavy and a light q-block each) where the causal cost model rates them faster
+    # causal D = 128 launches whose 256-row q-blocks fill one round: 128-row q-blocks on a persistent grid (one
+    # block per CU, a heavy and a light q-block each) where the causal cost model rates them faster
     assert plan(False, 1, 32, 2048, 2048, 128, True, 0) == (512, 1)
     assert plan(False, 2, 16, 2048, 2048, 128, True, 0) == (512, 1)
     assert plan(False, 1, 16, 4096, 4096, 128, True, 0) == (512, 1)
     assert plan(False, 1, 32, 1536, 1536, 128, True, 0) == (192, 1)   # a block would get two heavy q-blocks
-    assert plan(True, 1, 32, 2048, 2048, 128, True, 0) == (256, 1)    # the INT8 kernels keep 256-row q-blocks
+    assert plan(True, 1, 32, 2048, 2048, 128, True, 0) == (512, 1)    # the INT8 kernels too
+    assert plan(True, 1, 16, 4096, 4096, 128, True, 0) == (512, 1)
+    assert plan(True, 1, 12, 4096, 4096, 128, True, 0) == (384, 1)
+    assert plan(True, 1, 32, 1536, 1536, 128, True, 0) == (192, 1)
     assert plan(False, 1, 32, 4096, 4096, 128, True, 0) == (512, 1)   # two rounds of 256-row q-blocks
+    assert plan(True, 1, 32, 16384, 16384, 128, True, 0) == (2048, 1)  # NS: eight rounds, 256-row q-blocks
     # a workspace-size query agrees with the plan: (q-blocks - whole) * splits * 256 rows * (D + 1) fp32
     assert lib.sage_attn_workspace_bytes(1, 1, 3, 24576, 24576, 128, 0, 0) == 32 * 8 * 256 * 129 * 4
 

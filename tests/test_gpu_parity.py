@@ -341,6 +341,35 @@ def test_qfused_large_scales_on_causal_diagonal_tiles():
     _say(f"  worst |gpu-oracle| = {worst:.3g}")
 
 
+# ------------------------------------------------------------------ paired causal q-blocks
+PAIRED = [
+    Config("paired_b1h16_s4096", 1, 16, 16, 4096, 128, "bf16", "HND", True, False),
+    Config("paired_ragged_gqa_nhd", 1, 12, 4, 4000, 128, "fp16", "NHD", True, False),
+]
+
+
+@pytest.mark.parametrize("cfg", PAIRED, ids=lambda c: c.name)
+def test_paired_causal_schedule_parity(cfg):
+    """Causal D = 128 launches whose 256-row q-blocks fill one round run 128-row q-blocks on a persistent
+    grid of one block per CU (a heavy and a light q-block per block, in turn; the 2 x 16 and 12 x 32
+    128-row q-blocks here): sampled rows of every head against the oracle, and the Q-fused kernel equal
+    to the two-kernel path bit for bit."""
+    from sageattention import _capi
+
+    _say(f"[paired causal] {cfg}")
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        want = cfg.B * cfg.Hq * ((cfg.q_len + 127) // 128)
+        assert _capi.split_plan(True, cfg.B, cfg.Hq, cfg.q_len, cfg.S, cfg.D, True, 0) == (want, 1)
+    q, k, v = make_inputs(cfg, seed=17)
+    pro = gpu_prologue(cfg, q, k, v)
+    o = gpu_attn(cfg, pro, q.dtype)
+    rows = sample_rows(cfg.q_len, 24, np.random.default_rng(2))
+    worst = check_rows_vs_oracle(cfg, pro, o, range(cfg.Hq), rows, cfg.dtype)
+    o_f, _, _, _ = gpu_fused(cfg, q, k, v)
+    assert torch.equal(o_f, o), f"max diff {(o_f.float() - o.float()).abs().max().item()}"
+    _say(f"  worst |gpu-oracle| = {worst:.3g}")
+
+
 # ------------------------------------------------------------------ BASELINE sizes
 @pytest.mark.parametrize("cfg", BASELINE_CONFIGS, ids=lambda c: c.name)
 def test_baseline_config_parity(cfg):

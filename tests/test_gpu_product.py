@@ -122,6 +122,8 @@ CANARY = [
     Config("persistent_causal_d128", 1, 8, 8, 9000, 128, "bf16", "HND", True, False),
     # 360 q-blocks of 128 rows (D = 64 non-causal): the library's tail-split plan
     Config("tail_split_d64", 1, 20, 20, 2304, 64, "fp16", "NHD", False, False),
+    # 512 causal q-blocks of 128 rows paired on a persistent grid of one block per CU
+    Config("paired_causal_d128", 1, 16, 16, 4096, 128, "bf16", "HND", True, False),
 ]
 
 
