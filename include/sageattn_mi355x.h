@@ -176,12 +176,12 @@ int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* val
  * Key splits of the two entry points below (non-causal launches only).  A
  * launch has B*Hq*ceil(q_len/R) q-blocks, R = 128 query rows for head_dim 64
  * non-causal launches, for causal launches (every kind) whose 256-row
- * q-blocks would fill at most half the CUs, and for causal head_dim 128 direct
- * launches whose 256-row q-blocks fill at most one round when a cost model of
- * the schedule rates 128-row q-blocks faster; R = 256 otherwise (one block per
- * CU).  128-row blocks run two per CU, except the head_dim 128 direct
- * kernel's, whose LDS fits once per CU (more of them than CUs run as a
- * persistent grid, a heavy and a light causal q-block per block); for a non-causal
+ * q-blocks would fill at most half the CUs, and for causal launches whose
+ * 256-row q-blocks fill at most one round when a cost model of the schedule
+ * rates 128-row q-blocks faster; R = 256 otherwise (one block per CU).
+ * Non-causal 128-row blocks run two per CU, causal ones one per CU (more of
+ * them than CUs run as a persistent grid, a heavy and a light q-block per
+ * block); for a non-causal
  * launch that leaves compute units idle
  * (fewer blocks than CUs, or a last round partly filled) the key range of
  * some or all blocks can be split into parts whose fp32 partial outputs and

@@ -144,23 +144,28 @@ constexpr double kLoneHalfBlockTileI8 = 0.77;
 // 128-row q-blocks then fill twice as many, one block per CU; B1 H8 S4096
 // D128 INT8: -27%; the D = 128 direct kernel, whose 98 KB of LDS fits once per
 // CU, at B1 H8/H16 S1024-2048: -27% to -32%); w8 for the rest (a causal launch
-// of 2048 +4% in w4).  A causal D = 128 launch also runs w4 when its 256-row
+// of 2048 +4% in w4).  A causal launch also runs w4 when its 256-row
 // q-blocks fill one round and the causal cost model rates the 128-row q-blocks
 // faster: with one block resident per CU they run as a persistent grid in
 // which the snake schedule gives each block a heavy and a light q-block.
-// Direct kernel: B1 H32 S2048, B2 H16 S2048 -17%, B1 H24 S2048 -15%,
+// D = 128 direct kernel: B1 H32 S2048, B2 H16 S2048 -17%, B1 H24 S2048 -15%,
 // B1 H16 S4096 -21%; Q-fused INT8 kernel: B1 H16 S4096, B2 H8 S4096 -15%,
-// B1 H12 S4096 -19%, B1 H32 S2048 -10%.  The model keeps B1 H32 S1536 direct
-// in w8, where a block would get two heavy q-blocks (+15% in w4).
+// B1 H12 S4096 -19%, B1 H32 S2048 -10%; D = 64: direct B1 H32 S2048 -16%,
+// B1 H20 S3072 -5%, INT8 B1 H16 S4096 -16%, B1 H32 S2048 -9%.  The model
+// keeps B1 H32 S1536 D128 direct in w8, where a block would get two heavy
+// q-blocks (+15% in w4).
 bool small_blocks(int64_t head_dim, int is_causal, int64_t batch, int64_t q_heads, int64_t q_len, int64_t kv_len,
                   bool direct) {
   if (is_causal == 0) return head_dim == 64;
   const int64_t qblocks = batch * q_heads * ((q_len + 255) / 256);
   if (qblocks <= 0) return false;
   if (qblocks * 2 <= device_cus()) return true;
-  if (head_dim != 128 || qblocks > device_cus()) return false;
-  return (direct ? kLoneHalfBlockTileDirect : kLoneHalfBlockTileI8) *
-             w4::causal_blocks_cost<128, w4::kQkBf16>(batch * q_heads, q_len, kv_len) <
+  if (qblocks > device_cus()) return false;
+  const double f = direct ? kLoneHalfBlockTileDirect : kLoneHalfBlockTileI8;
+  if (head_dim == 64)
+    return f * w4::causal_blocks_cost<64, w4::kQkBf16>(batch * q_heads, q_len, kv_len) <
+           w8::causal_blocks_cost<64, w8::kQkBf16>(batch * q_heads, q_len, kv_len);
+  return f * w4::causal_blocks_cost<128, w4::kQkBf16>(batch * q_heads, q_len, kv_len) <
          w8::causal_blocks_cost<128, w8::kQkBf16>(batch * q_heads, q_len, kv_len);
 }
 

@@ -461,6 +461,8 @@ def test_automatic_plans_for_256_cus(lib):
     assert plan(True, 1, 32, 1536, 1536, 128, True, 0) == (192, 1)
     assert plan(False, 1, 32, 4096, 4096, 128, True, 0) == (512, 1)   # two rounds of 256-row q-blocks
     assert plan(True, 1, 32, 16384, 16384, 128, True, 0) == (2048, 1)  # NS: eight rounds, 256-row q-blocks
+    assert plan(False, 1, 32, 2048, 2048, 64, True, 0) == (512, 1)     # head_dim 64 too
+    assert plan(True, 1, 16, 4096, 4096, 64, True, 0) == (512, 1)
     # a workspace-size query agrees with the plan: (q-blocks - whole) * splits * 256 rows * (D + 1) fp32
     assert lib.sage_attn_workspace_bytes(1, 1, 3, 24576, 24576, 128, 0, 0) == 32 * 8 * 256 * 129 * 4
 

@@ -156,10 +156,11 @@ def test_direct_dispatch_range_sampled_rows(cfg):
 @pytest.mark.parametrize("cfg", [
     Config("paired_b1h32_s2048", 1, 32, 32, 2048, 128, "bf16", "HND", True, False),
     Config("paired_b2h16_s2048_nhd_gqa", 2, 16, 4, 2048, 128, "fp16", "NHD", True, False),
+    Config("paired_d64_b1h32_s2048", 1, 32, 32, 2048, 64, "fp16", "HND", True, False),
 ], ids=lambda c: c.name)
 def test_direct_causal_paired_schedule(cfg):
-    """Causal D = 128 direct launches whose 256-row q-blocks fill one round run 128-row q-blocks as a
-    persistent grid of one block per CU, each block a heavy and a light q-block in turn: every output
+    """Causal direct launches whose 256-row q-blocks fill one round run 128-row q-blocks as a persistent
+    grid of one block per CU, each block a heavy and a light q-block in turn: every output
     element and LSE written (NaN canaries), sampled rows of every head against the oracle, and the LSE
     of those rows."""
     from sageattention import _capi, ops

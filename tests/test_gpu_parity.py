@@ -345,15 +345,16 @@ def test_qfused_large_scales_on_causal_diagonal_tiles():
 PAIRED = [
     Config("paired_b1h16_s4096", 1, 16, 16, 4096, 128, "bf16", "HND", True, False),
     Config("paired_ragged_gqa_nhd", 1, 12, 4, 4000, 128, "fp16", "NHD", True, False),
+    Config("paired_d64", 1, 16, 16, 4096, 64, "fp16", "HND", True, False),
 ]
 
 
 @pytest.mark.parametrize("cfg", PAIRED, ids=lambda c: c.name)
 def test_paired_causal_schedule_parity(cfg):
-    """Causal D = 128 launches whose 256-row q-blocks fill one round run 128-row q-blocks on a persistent
-    grid of one block per CU (a heavy and a light q-block per block, in turn; the 2 x 16 and 12 x 32
-    128-row q-blocks here): sampled rows of every head against the oracle, and the Q-fused kernel equal
-    to the two-kernel path bit for bit."""
+    """Causal launches whose 256-row q-blocks fill one round run 128-row q-blocks on a persistent grid of
+    one block per CU (a heavy and a light q-block per block, in turn; 512, 384 and 512 128-row q-blocks
+    here): sampled rows of every head against the oracle, and the Q-fused kernel equal to the two-kernel
+    path bit for bit."""
     from sageattention import _capi
 
     _say(f"[paired causal] {cfg}")
