@@ -245,10 +245,11 @@ extern "C" int sage_attn_i8_fwd(const int8_t* q_i8, const int8_t* k_i8, const vo
                                 int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_n,
                                 int is_causal, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8, q_i8, k_i8, value_t, out, nullptr, q_scale,
-                  k_scale, out_dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_heads * q_len * head_dim,
-                  q_len * head_dim, head_dim, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0,
-                  o_stride_b, o_stride_h, o_stride_n, is_causal, 0.0, 1, nullptr, 0, stream, "sage_attn_i8_fwd");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8, q_i8, k_i8, value_t, out, nullptr,
+                  q_scale, k_scale, out_dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim,
+                  q_heads * q_len * head_dim, q_len * head_dim, head_dim, kv_heads * kv_len * head_dim,
+                  kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n, is_causal, 0.0, 1, nullptr,
+                  0, stream, "sage_attn_i8_fwd");
 }
 
 extern "C" int sage_attn_i8_fwd_lse(const int8_t* q_i8, const int8_t* k_i8, const void* value_t, void* out,
@@ -273,11 +274,11 @@ extern "C" int sage_attn_direct_fwd(const void* query, const void* key, const vo
                                     int is_causal, double sm_scale, int num_splits, void* workspace,
                                     int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, dtype == SAGE_DTYPE_BF16 ? w8::kQkBf16 : w8::kQkF16,
-                  query, key, value_t, out, lse, nullptr, nullptr, dtype, batch, q_heads, kv_heads, q_len, kv_len,
-                  head_dim, q_stride_b, q_stride_h, q_stride_n, k_stride_b, k_stride_h, k_stride_n, 0, 0, 0,
-                  o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes,
-                  stream, "sage_attn_direct_fwd");
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len,
+                  dtype == SAGE_DTYPE_BF16 ? w8::kQkBf16 : w8::kQkF16, query, key, value_t, out, lse, nullptr, nullptr,
+                  dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h, q_stride_n,
+                  k_stride_b, k_stride_h, k_stride_n, 0, 0, 0, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale,
+                  num_splits, workspace, workspace_bytes, stream, "sage_attn_direct_fwd");
 }
 
 extern "C" int sage_attn_direct_fwd_vrows(const void* query, const void* key, const void* value, void* out,
@@ -306,8 +307,8 @@ extern "C" int sage_attn_i8_fwd_qfused(const void* query, const int8_t* k_i8, co
                                        int is_causal, double sm_scale, int num_splits, void* workspace,
                                        int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
-                  k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8F, query, k_i8, value_t, out, lse,
+                  nullptr, k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
                   q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b,
                   o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace, workspace_bytes, stream,
                   "sage_attn_i8_fwd_qfused");
@@ -323,8 +324,8 @@ extern "C" int sage_attn_i8_fwd_qfused_vrows(const void* query, const int8_t* k_
                                              int is_causal, double sm_scale, int num_splits, void* workspace,
                                              int64_t workspace_bytes, void* stream) {
   clear_error();
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8FV, query, k_i8, value, out, lse, nullptr,
-                  k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8FV, query, k_i8, value, out, lse,
+                  nullptr, k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
                   q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, v_stride_b, v_stride_h,
                   v_stride_n, o_stride_b, o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, workspace,
                   workspace_bytes, stream, "sage_attn_i8_fwd_qfused_vrows");
@@ -356,8 +357,8 @@ extern "C" int sage_attn_i8_fwd_qfused_noalloc(const void* query, const int8_t* 
     ws = scratch_address(fn);
     if (ws == nullptr) return SAGE_ERR_HIP;
   }
-  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8F, query, k_i8, value_t, out, lse, nullptr,
-                  k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
+  return run_attn(head_dim, is_causal, batch, q_heads, q_len, kv_len, w8::kQkI8F, query, k_i8, value_t, out, lse,
+                  nullptr, k_scale, dtype, batch, q_heads, kv_heads, q_len, kv_len, head_dim, q_stride_b, q_stride_h,
                   q_stride_n, kv_heads * kv_len * head_dim, kv_len * head_dim, head_dim, 0, 0, 0, o_stride_b,
                   o_stride_h, o_stride_n, is_causal, sm_scale, num_splits, ws, ws != nullptr ? kScratchBytes : 0,
                   stream, fn);
