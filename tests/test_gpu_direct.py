@@ -157,6 +157,7 @@ def test_direct_dispatch_range_sampled_rows(cfg):
     Config("paired_b1h32_s2048", 1, 32, 32, 2048, 128, "bf16", "HND", True, False),
     Config("paired_b2h16_s2048_nhd_gqa", 2, 16, 4, 2048, 128, "fp16", "NHD", True, False),
     Config("paired_d64_b1h32_s2048", 1, 32, 32, 2048, 64, "fp16", "HND", True, False),
+    Config("paired_cross_q2048_kv4096", 1, 32, 32, 4096, 128, "bf16", "HND", True, False, Sq=2048),
 ], ids=lambda c: c.name)
 def test_direct_causal_paired_schedule(cfg):
     """Causal direct launches whose 256-row q-blocks fill one round run 128-row q-blocks as a persistent
@@ -167,14 +168,15 @@ def test_direct_causal_paired_schedule(cfg):
 
     _say(f"[direct paired] {cfg}")
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
-        assert _capi.split_plan(False, cfg.B, cfg.Hq, cfg.S, cfg.S, cfg.D, True, 0) == (cfg.B * cfg.Hq * cfg.S // 128, 1)
+        want = cfg.B * cfg.Hq * ((cfg.q_len + 127) // 128)
+        assert _capi.split_plan(False, cfg.B, cfg.Hq, cfg.q_len, cfg.S, cfg.D, True, 0) == (want, 1)
     q, k, v = make_inputs(cfg, seed=16)
     lay = ops.HND if cfg.layout == "HND" else ops.NHD
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     vt = torch.empty(cfg.B, cfg.Hkv, cfg.D, cfg.S, device="cuda", dtype=torch.float16)
     ops.v_transpose(vd, vt, lay)
     o = torch.full(qd.shape, float("nan"), device="cuda", dtype=qd.dtype)
-    lse = torch.full((cfg.B, cfg.Hq, cfg.S), float("nan"), device="cuda", dtype=torch.float32)
+    lse = torch.full((cfg.B, cfg.Hq, cfg.q_len), float("nan"), device="cuda", dtype=torch.float32)
     fn = ops.bf16_attn_t if cfg.dtype == "bf16" else ops.fp16_attn_t
     fn(qd, kd, vt, o, lay, 1, cfg.D ** -0.5, 0, lse=lse)
     torch.cuda.synchronize()

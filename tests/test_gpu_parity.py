@@ -346,13 +346,16 @@ PAIRED = [
     Config("paired_b1h16_s4096", 1, 16, 16, 4096, 128, "bf16", "HND", True, False),
     Config("paired_ragged_gqa_nhd", 1, 12, 4, 4000, 128, "fp16", "NHD", True, False),
     Config("paired_d64", 1, 16, 16, 4096, 64, "fp16", "HND", True, False),
+    # fewer queries than keys (top-left causal: keys past the last query row are never seen)
+    Config("paired_cross_q2048_kv3000", 1, 32, 32, 3000, 128, "bf16", "HND", True, False, Sq=2048),
+    Config("paired_d64_cross_q4096_kv8192", 1, 16, 16, 8192, 64, "fp16", "HND", True, False, Sq=4096),
 ]
 
 
 @pytest.mark.parametrize("cfg", PAIRED, ids=lambda c: c.name)
 def test_paired_causal_schedule_parity(cfg):
     """Causal launches whose 256-row q-blocks fill one round run 128-row q-blocks on a persistent grid of
-    one block per CU (a heavy and a light q-block per block, in turn; 512, 384 and 512 128-row q-blocks
+    one block per CU (a heavy and a light q-block per block, in turn; 384 or 512 128-row q-blocks
     here): sampled rows of every head against the oracle, and the Q-fused kernel equal to the two-kernel
     path bit for bit."""
     from sageattention import _capi
