@@ -245,29 +245,32 @@ class TestApiContract:
         assert sageattn(q, k, k).shape == q.shape
 
     @pytest.mark.parametrize("smooth_k", [False, True])
-    def test_hip_graph_capture_and_replay(self, sageattn, smooth_k):
+    @pytest.mark.parametrize("heads,seq_len,causal", [(4, 1000, False), (32, 2048, True)])
+    def test_hip_graph_capture_and_replay(self, sageattn, smooth_k, heads, seq_len, causal):
         # the launches of a call allocate from the caller's torch allocator and never memset or synchronise,
-        # so a call captured in a HIP graph replays to the eager result; here the plan splits the keys (16
-        # q-blocks on a full device), so the graph also holds the workspace and the merge launch, and with
-        # smooth_k the K mean's chunk-sum launch and its workspace
-        q, k, v = (randn(1, 4, 1000, 128) for _ in range(3))
+        # so a call captured in a HIP graph replays to the eager result.  H4 S1000: the plan splits the keys
+        # (16 q-blocks on a full device), so the graph also holds the workspace and the merge launch, and with
+        # smooth_k the K mean's chunk-sum launch and its workspace.  H32 S2048 causal: 512 128-row q-blocks
+        # on the persistent grid, heavy and light paired.
+        q, k, v = (randn(1, heads, seq_len, 128) for _ in range(3))
         k = k + 3.0  # a K offset that smooth_k removes
-        ref = sageattn(q, k, v, smooth_k=smooth_k)
+        ref = sageattn(q, k, v, is_causal=causal, smooth_k=smooth_k)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            sageattn(q, k, v, smooth_k=smooth_k)
+            sageattn(q, k, v, is_causal=causal, smooth_k=smooth_k)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            out = sageattn(q, k, v, smooth_k=smooth_k)
+            out = sageattn(q, k, v, is_causal=causal, smooth_k=smooth_k)
         for _ in range(3):
             out.zero_()
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(out, ref)
-            assert torch.equal(sageattn(q, k, v, smooth_k=smooth_k), ref)  # eager work between the replays
+            # eager work between the replays
+            assert torch.equal(sageattn(q, k, v, is_causal=causal, smooth_k=smooth_k), ref)
 
     def test_empty_keys(self, sageattn):
         # no key at all: every row's output is 0 and its log-sum-exp -inf (the oracle's convention)
